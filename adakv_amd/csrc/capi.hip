@@ -1,0 +1,409 @@
+// extern "C" entry points of libadakv_amd.so: argument validation on the host,
+// workspace carving, kernel launches on the caller's stream.  Nothing here
+// allocates device memory or waits on the device.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "adakv_amd.h"
+#include "internal.hpp"
+
+namespace adakv {
+namespace {
+
+constexpr size_t kAlign = 256;
+constexpr int kMaxBlocks = 32768;
+constexpr int kMaxSparseSplits = 16;      // the in-kernel merge reads at most 16 partials
+constexpr int kSparseMinPer = 32;         // blocks a sparse split takes at least
+constexpr int kMaxDenseSplits = 256;
+constexpr int kDenseBlocksPerSplit = 128;
+constexpr size_t kLdsLimit = 65536;
+constexpr int kMaxPlanCounters = 4096;                  // one per sequence
+constexpr int kMaxDecodeCounters = 12288;               // one per (sequence, KV head)
+constexpr size_t kCounterBytes = (size_t)(kMaxPlanCounters + kMaxDecodeCounters) * 4;
+
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+int ceil_div_h(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+bool valid_dtype(int dt) { return dt == ADAKV_F32 || dt == ADAKV_F16 || dt == ADAKV_BF16; }
+int elt_bytes(int dt) { return dt == ADAKV_F32 ? 4 : 2; }
+int per_vec(int dt) { return 16 / elt_bytes(dt); }
+int gmax_of(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8; }
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Centroid element type per key element type: the key type itself or fp32
+// (fp32 keys may also be summarised in bf16).
+bool centroid_pair_ok(int kdt, int cdt) {
+  if (cdt == ADAKV_F32) return true;
+  if (kdt == ADAKV_F32) return cdt == ADAKV_BF16;
+  return kdt == cdt;
+}
+
+int check_geometry(const adakv_geometry_t* g) {
+  if (!g) return ADAKV_ERR_NULL;
+  if (g->batch < 1 || g->n_q_heads < 1 || g->n_kv_heads < 1 || g->block_size < 1 ||
+      g->max_seq_len < 1 || g->max_blocks < 1)
+    return ADAKV_ERR_SHAPE;
+  if (g->n_q_heads % g->n_kv_heads) return ADAKV_ERR_SHAPE;
+  if ((int64_t)g->max_blocks * g->block_size < g->max_seq_len) return ADAKV_ERR_SHAPE;
+  if (g->n_q_heads / g->n_kv_heads > 8) return ADAKV_ERR_UNSUPPORTED;
+  const int D = g->head_dim;
+  if (D != 32 && D != 64 && D != 128 && D != 256) return ADAKV_ERR_UNSUPPORTED;
+  if (g->max_blocks > kMaxBlocks || g->block_size > 4096) return ADAKV_ERR_UNSUPPORTED;
+  if (g->batch > kMaxPlanCounters || (int64_t)g->batch * g->n_kv_heads > kMaxDecodeCounters)
+    return ADAKV_ERR_UNSUPPORTED;
+  return ADAKV_OK;
+}
+
+int check_kv(const adakv_geometry_t* g, const adakv_kv_t* kv, bool need_v) {
+  if (!kv || !kv->k || (need_v && !kv->v)) return ADAKV_ERR_NULL;
+  if (!valid_dtype(kv->dtype)) return ADAKV_ERR_DTYPE;
+  const int e = per_vec(kv->dtype);
+  if (!aligned16(kv->k) || (need_v && !aligned16(kv->v))) return ADAKV_ERR_VALUE;
+  if (kv->stride_b % e || kv->stride_h % e || kv->stride_s % e) return ADAKV_ERR_VALUE;
+  if (kv->stride_b < 0 || kv->stride_h < 0 || kv->stride_s < 0) return ADAKV_ERR_VALUE;
+  (void)g;
+  return ADAKV_OK;
+}
+
+int check_q(const adakv_query_t* q) {
+  if (!q || !q->data) return ADAKV_ERR_NULL;
+  if (!valid_dtype(q->dtype)) return ADAKV_ERR_DTYPE;
+  return ADAKV_OK;
+}
+
+int check_out(const adakv_output_t* o) {
+  if (!o || !o->data) return ADAKV_ERR_NULL;
+  if (!valid_dtype(o->dtype)) return ADAKV_ERR_DTYPE;
+  return ADAKV_OK;
+}
+
+int check_centroid(const adakv_centroid_t* c) {
+  if (!c || !c->data) return ADAKV_ERR_NULL;
+  if (!valid_dtype(c->dtype)) return ADAKV_ERR_DTYPE;
+  if (!aligned16(c->data)) return ADAKV_ERR_VALUE;
+  return ADAKV_OK;
+}
+
+int check_budget(const adakv_budget_t* p) {
+  if (!p) return ADAKV_ERR_NULL;
+  if (p->policy != ADAKV_POLICY_FIXED && p->policy != ADAKV_POLICY_ADAPTIVE) return ADAKV_ERR_VALUE;
+  if (!isfinite(p->avg_budget) || !isfinite(p->temperature)) return ADAKV_ERR_VALUE;
+  if (p->k_min < 0 || p->k_max < 0 || p->n_sink_blocks < 0 || p->n_local_blocks < 0 || p->c_min < 0)
+    return ADAKV_ERR_VALUE;
+  return ADAKV_OK;
+}
+
+int check_ws(const adakv_geometry_t* g, int T, void* ws, size_t bytes) {
+  if (!ws) return ADAKV_ERR_NULL;
+  if (((uintptr_t)ws & (kAlign - 1)) != 0) return ADAKV_ERR_WORKSPACE;
+  if (bytes < workspace_layout(*g, T).total) return ADAKV_ERR_WORKSPACE;
+  return ADAKV_OK;
+}
+
+int table_width_of(const adakv_geometry_t* g, const adakv_budget_t* p) {
+  int64_t w = p->k_max;
+  const int64_t f = (int64_t)p->n_sink_blocks + p->n_local_blocks + p->c_min;
+  if (f > w) w = f;
+  if (w > g->max_blocks) w = g->max_blocks;
+  if (w < 1) w = 1;
+  return (int)w;
+}
+
+int64_t union_max(const adakv_geometry_t& g, int T) {
+  return std::min<int64_t>((int64_t)(g.n_q_heads / g.n_kv_heads) * T, g.max_blocks);
+}
+
+int list_cap_of(const adakv_geometry_t& g, int T, int nsplit) {
+  const int64_t umax = union_max(g, T);
+  return (int)std::max<int64_t>(1, std::max<int64_t>(ceil_div_h(umax, nsplit),
+                                                     std::min<int64_t>(kSparseMinPer, umax)));
+}
+
+// LDS of the decode kernel: static arrays (sized for 8 waves) plus, in sparse
+// mode, the weights, the union bitmap and the block list.
+size_t decode_lds_bytes(const adakv_geometry_t& g, int list_cap, bool sparse) {
+  const int GM = gmax_of(g.n_q_heads / g.n_kv_heads), D = g.head_dim, NW = 8;
+  const int hc = std::max(1, std::min(GM, 8192 / (NW * D)));
+  const size_t stat = (size_t)GM * D * 4 + (size_t)NW * hc * D * 4 + (size_t)2 * NW * GM * 4 + 256;
+  const size_t dyn = sparse ? ((size_t)g.n_q_heads * 8 + 15) / 16 * 16 +
+                                  (size_t)(((g.max_blocks + 3) / 4) + list_cap) * 4
+                            : 16;
+  return stat + dyn;
+}
+
+BudgetCfg budget_cfg(const adakv_budget_t* p) {
+  BudgetCfg c;
+  c.avg = p->avg_budget;
+  c.k_min = p->k_min; c.k_max = p->k_max;
+  c.sink = p->n_sink_blocks; c.local = p->n_local_blocks; c.c_min = p->c_min;
+  c.policy = p->policy;
+  c.temperature = p->temperature;
+  return c;
+}
+
+int status_of(hipError_t e) { return e == hipSuccess ? ADAKV_OK : ADAKV_ERR_LAUNCH; }
+
+CentroidArgs centroid_args(const adakv_geometry_t* g, const adakv_kv_t* kv, const int32_t* lens,
+                           const adakv_centroid_t* c, int n_new) {
+  CentroidArgs a{};
+  a.k = kv->k;
+  a.sb = kv->stride_b; a.sh = kv->stride_h; a.ss = kv->stride_s;
+  a.c = c->data;
+  a.seq_lens = lens;
+  a.uniform_len = g->max_seq_len;
+  a.B = g->batch; a.Hkv = g->n_kv_heads; a.bs = g->block_size; a.max_blocks = g->max_blocks;
+  a.n_new = n_new;
+  return a;
+}
+
+ScoreArgs score_args(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_centroid_t* c,
+                     const int32_t* lens, float* scores, int sp) {
+  ScoreArgs sa{};
+  sa.q = q->data; sa.qdt = q->dtype; sa.qsb = q->stride_b; sa.qsh = q->stride_h;
+  sa.c = c->data; sa.max_blocks = g->max_blocks;
+  sa.seq_lens = lens; sa.uniform_len = g->max_seq_len; sa.bs = g->block_size;
+  sa.B = g->batch; sa.Hq = g->n_q_heads; sa.Hkv = g->n_kv_heads; sa.G = g->n_q_heads / g->n_kv_heads;
+  sa.scores = scores; sa.sp = sp;
+  return sa;
+}
+
+// Scores (with an optional fused centroid append) and the per-head selection;
+// sel_lens come from the budget kernel when requested, otherwise the decode
+// kernel derives them from the weights left in the workspace.
+int run_plan(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_centroid_t* c,
+             const adakv_kv_t* kv_append, int n_new, const int32_t* lens, const adakv_budget_t* p,
+             int32_t* table, int T, int32_t* sel_lens, char* ws, hipStream_t s) {
+  const WorkspaceLayout L = workspace_layout(*g, T);
+  ScoreArgs sa = score_args(g, q, c, lens, reinterpret_cast<float*>(ws + L.scores), L.sp);
+  if (n_new > 0) {
+    sa.n_new = n_new;
+    sa.k = kv_append->k; sa.kdt = kv_append->dtype;
+    sa.ksb = kv_append->stride_b; sa.ksh = kv_append->stride_h; sa.kss = kv_append->stride_s;
+  }
+  if (launch_score(sa, c->dtype, g->head_dim, s) != hipSuccess) return ADAKV_ERR_LAUNCH;
+  SelectArgs se{};
+  se.scores = sa.scores; se.sp = L.sp;
+  se.seq_lens = lens; se.uniform_len = g->max_seq_len; se.bs = g->block_size;
+  se.B = g->batch; se.Hq = g->n_q_heads;
+  se.cfg = budget_cfg(p);
+  se.table = table; se.T = T;
+  se.wbuf = reinterpret_cast<double*>(ws + L.weights);
+  if (launch_select(se, g->max_blocks, s) != hipSuccess) return ADAKV_ERR_LAUNCH;
+  if (!sel_lens) return ADAKV_OK;
+  BudgetArgs ba{};
+  ba.wbuf = se.wbuf;
+  ba.seq_lens = lens; ba.uniform_len = g->max_seq_len; ba.bs = g->block_size;
+  ba.B = g->batch; ba.Hq = g->n_q_heads;
+  ba.cfg = se.cfg;
+  ba.sel_lens = sel_lens;
+  return status_of(launch_budget(ba, s));
+}
+
+// Table-driven sparse decode (table != nullptr) or dense decode (+ merge).
+// With sel_lens == nullptr the per-head counts are derived from the budget
+// weights in the workspace and written to sel_lens_out.
+int run_decode(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
+               const int32_t* lens, const int32_t* table, int T, const int32_t* sel_lens,
+               const adakv_budget_t* p, int32_t* sel_lens_out, float sm_scale,
+               const adakv_output_t* out, char* ws, int T_layout, hipStream_t s) {
+  const WorkspaceLayout L = workspace_layout(*g, T_layout);
+  DecodeArgs d{};
+  d.q = q->data; d.qdt = q->dtype; d.qsb = q->stride_b; d.qsh = q->stride_h;
+  d.k = kv->k; d.v = kv->v; d.sb = kv->stride_b; d.sh = kv->stride_h; d.ss = kv->stride_s;
+  d.seq_lens = lens; d.uniform_len = g->max_seq_len; d.bs = g->block_size;
+  d.B = g->batch; d.Hq = g->n_q_heads; d.Hkv = g->n_kv_heads; d.G = g->n_q_heads / g->n_kv_heads;
+  d.table = table; d.T = T; d.sel_lens = sel_lens;
+  d.wbuf = reinterpret_cast<const double*>(ws + L.weights);
+  if (p) d.cfg = budget_cfg(p);
+  d.sel_lens_out = sel_lens_out;
+  d.scale_log2 = sm_scale * 1.4426950408889634f;
+  d.out = out->data; d.odt = out->dtype; d.osb = out->stride_b; d.osh = out->stride_h;
+  d.partials = reinterpret_cast<float*>(ws + L.partials);
+  d.counters = reinterpret_cast<int*>(ws + L.counters_dec);
+  d.max_blocks = g->max_blocks;
+  if (table) {
+    d.nsplit = L.nsplit_sparse;
+    d.min_per = kSparseMinPer;
+    d.list_cap = list_cap_of(*g, T, d.nsplit);
+    d.merge_in_kernel = 1;
+  } else {
+    d.nsplit = L.nsplit_dense;
+    d.min_per = 1;
+    d.list_cap = 0;
+    d.merge_in_kernel = 0;
+  }
+  if (decode_lds_bytes(*g, d.list_cap, table != nullptr) > kLdsLimit) return ADAKV_ERR_UNSUPPORTED;
+  if (launch_decode(d, kv->dtype, g->head_dim, s) != hipSuccess) return ADAKV_ERR_LAUNCH;
+  if (table) return ADAKV_OK;
+  MergeArgs m{};
+  m.partials = d.partials; m.nsplit = d.nsplit;
+  m.B = d.B; m.Hq = d.Hq; m.Hkv = d.Hkv; m.G = d.G; m.D = g->head_dim;
+  m.seq_lens = lens; m.uniform_len = g->max_seq_len; m.bs = g->block_size;
+  m.out = out->data; m.odt = out->dtype; m.osb = out->stride_b; m.osh = out->stride_h;
+  return status_of(launch_merge(m, s));
+}
+
+}  // namespace
+
+WorkspaceLayout workspace_layout(const adakv_geometry_t& g, int T) {
+  WorkspaceLayout L{};
+  const int G = g.n_q_heads / g.n_kv_heads;
+  L.sp = (g.max_blocks + 3) / 4 * 4;
+  const int64_t umax = union_max(g, T);
+  L.nsplit_sparse = (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div_h(umax, kSparseMinPer),
+                                                                kMaxSparseSplits));
+  L.nsplit_dense = std::max(1, std::min(ceil_div_h(g.max_blocks, kDenseBlocksPerSplit), kMaxDenseSplits));
+  L.nsplit_max = std::max(L.nsplit_sparse, L.nsplit_dense);
+  // The counters sit at fixed offsets so that they stay zero however the
+  // geometry of successive calls on one workspace changes; everything after
+  // them is scratch that every call fully rewrites before reading.
+  L.counters_plan = 0;
+  L.counters_dec = (size_t)kMaxPlanCounters * 4;
+  size_t off = kCounterBytes;
+  L.scores = off;        off = align_up(off + (size_t)g.batch * g.n_q_heads * L.sp * 4);
+  L.weights = off;       off = align_up(off + (size_t)g.batch * g.n_q_heads * 8);
+  L.partials = off;
+  off = align_up(off + (size_t)g.batch * g.n_kv_heads * L.nsplit_max * G * (g.head_dim + 2) * 4);
+  L.table = off;         off = align_up(off + (size_t)g.batch * g.n_q_heads * T * 4);
+  L.lens = off;          off = align_up(off + (size_t)g.batch * g.n_q_heads * 4);
+  L.total = off;
+  return L;
+}
+
+}  // namespace adakv
+
+using namespace adakv;
+
+extern "C" {
+
+const char* adakv_status_string(int status) {
+  switch (status) {
+    case ADAKV_OK: return "ok";
+    case ADAKV_ERR_NULL: return "a required pointer is NULL";
+    case ADAKV_ERR_SHAPE: return "inconsistent shapes";
+    case ADAKV_ERR_DTYPE: return "unsupported or mismatched dtype";
+    case ADAKV_ERR_UNSUPPORTED: return "configuration not supported by the built kernels";
+    case ADAKV_ERR_WORKSPACE: return "workspace too small or misaligned";
+    case ADAKV_ERR_LAUNCH: return "HIP kernel launch failed";
+    case ADAKV_ERR_VALUE: return "invalid parameter value or alignment";
+    default: return "unknown status";
+  }
+}
+
+int adakv_abi_version(void) { return ADAKV_ABI_VERSION; }
+
+int32_t adakv_table_width(const adakv_geometry_t* g, const adakv_budget_t* p) {
+  if (check_geometry(g) != ADAKV_OK || check_budget(p) != ADAKV_OK) return -1;
+  return table_width_of(g, p);
+}
+
+size_t adakv_workspace_bytes(const adakv_geometry_t* g, int32_t table_width) {
+  if (check_geometry(g) != ADAKV_OK || table_width < 1) return 0;
+  return workspace_layout(*g, table_width).total;
+}
+
+int adakv_centroid_build(const adakv_geometry_t* g, const adakv_kv_t* kv, const int32_t* seq_lens,
+                         const adakv_centroid_t* c, void* stream) {
+  int st;
+  if ((st = check_geometry(g)) || (st = check_kv(g, kv, false)) || (st = check_centroid(c))) return st;
+  if (!centroid_pair_ok(kv->dtype, c->dtype)) return ADAKV_ERR_DTYPE;
+  CentroidArgs a = centroid_args(g, kv, seq_lens, c, 0);
+  return status_of(launch_centroid(a, kv->dtype, c->dtype, g->head_dim, (hipStream_t)stream));
+}
+
+int adakv_centroid_append(const adakv_geometry_t* g, const adakv_kv_t* kv, const int32_t* seq_lens,
+                          int32_t n_new, const adakv_centroid_t* c, void* stream) {
+  int st;
+  if ((st = check_geometry(g)) || (st = check_kv(g, kv, false)) || (st = check_centroid(c))) return st;
+  if (n_new < 1 || n_new > g->max_seq_len) return ADAKV_ERR_VALUE;
+  if (!centroid_pair_ok(kv->dtype, c->dtype)) return ADAKV_ERR_DTYPE;
+  CentroidArgs a = centroid_args(g, kv, seq_lens, c, n_new);
+  return status_of(launch_centroid(a, kv->dtype, c->dtype, g->head_dim, (hipStream_t)stream));
+}
+
+int adakv_block_scores(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_centroid_t* c,
+                       const int32_t* seq_lens, float* scores, int32_t pitch, void* stream) {
+  int st;
+  if ((st = check_geometry(g)) || (st = check_q(q)) || (st = check_centroid(c))) return st;
+  if (!scores) return ADAKV_ERR_NULL;
+  if (pitch < g->max_blocks) return ADAKV_ERR_SHAPE;
+  ScoreArgs sa = score_args(g, q, c, seq_lens, scores, pitch);
+  return status_of(launch_score(sa, c->dtype, g->head_dim, (hipStream_t)stream));
+}
+
+int adakv_plan(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_centroid_t* c,
+               const int32_t* seq_lens, const adakv_budget_t* p, const adakv_selection_t* sel,
+               void* ws, size_t ws_bytes, void* stream) {
+  int st;
+  if ((st = check_geometry(g)) || (st = check_q(q)) || (st = check_centroid(c)) ||
+      (st = check_budget(p)))
+    return st;
+  if (!sel || !sel->block_table || !sel->sel_lens) return ADAKV_ERR_NULL;
+  const int T = table_width_of(g, p);
+  if (sel->table_width < T) return ADAKV_ERR_SHAPE;
+  if ((st = check_ws(g, sel->table_width, ws, ws_bytes))) return st;
+  return run_plan(g, q, c, nullptr, 0, seq_lens, p, sel->block_table, sel->table_width,
+                  sel->sel_lens, reinterpret_cast<char*>(ws), (hipStream_t)stream);
+}
+
+int adakv_sparse_decode(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
+                        const int32_t* seq_lens, const adakv_selection_t* sel, float sm_scale,
+                        const adakv_output_t* out, void* ws, size_t ws_bytes, void* stream) {
+  int st;
+  if ((st = check_geometry(g)) || (st = check_q(q)) || (st = check_kv(g, kv, true)) ||
+      (st = check_out(out)))
+    return st;
+  if (!sel || !sel->block_table || !sel->sel_lens) return ADAKV_ERR_NULL;
+  if (sel->table_width < 1) return ADAKV_ERR_SHAPE;
+  if (!isfinite(sm_scale)) return ADAKV_ERR_VALUE;
+  if ((st = check_ws(g, sel->table_width, ws, ws_bytes))) return st;
+  return run_decode(g, q, kv, seq_lens, sel->block_table, sel->table_width, sel->sel_lens,
+                    nullptr, nullptr, sm_scale, out, reinterpret_cast<char*>(ws),
+                    sel->table_width, (hipStream_t)stream);
+}
+
+int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
+                       const adakv_centroid_t* c, const int32_t* seq_lens,
+                       const adakv_budget_t* p, const adakv_selection_t* sel, int32_t append_new,
+                       float sm_scale, const adakv_output_t* out, void* ws, size_t ws_bytes,
+                       void* stream) {
+  int st;
+  if ((st = check_geometry(g)) || (st = check_q(q)) || (st = check_kv(g, kv, true)) ||
+      (st = check_centroid(c)) || (st = check_budget(p)) || (st = check_out(out)))
+    return st;
+  if (append_new < 0 || append_new > g->max_seq_len) return ADAKV_ERR_VALUE;
+  if (!isfinite(sm_scale)) return ADAKV_ERR_VALUE;
+  const int T = table_width_of(g, p);
+  int Tl = T;
+  if (sel) {
+    if (!sel->block_table || !sel->sel_lens) return ADAKV_ERR_NULL;
+    if (sel->table_width < T) return ADAKV_ERR_SHAPE;
+    Tl = sel->table_width;
+  }
+  if ((st = check_ws(g, Tl, ws, ws_bytes))) return st;
+  char* w = reinterpret_cast<char*>(ws);
+  const WorkspaceLayout L = workspace_layout(*g, Tl);
+  int32_t* table = sel ? sel->block_table : reinterpret_cast<int32_t*>(w + L.table);
+  int32_t* lens = sel ? sel->sel_lens : reinterpret_cast<int32_t*>(w + L.lens);
+  const hipStream_t s = (hipStream_t)stream;
+  if (append_new > 0 && !centroid_pair_ok(kv->dtype, c->dtype)) return ADAKV_ERR_DTYPE;
+  if ((st = run_plan(g, q, c, kv, append_new, seq_lens, p, table, Tl, nullptr, w, s))) return st;
+  return run_decode(g, q, kv, seq_lens, table, Tl, nullptr, p, lens, sm_scale, out, w, Tl, s);
+}
+
+int adakv_dense_decode(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
+                       const int32_t* seq_lens, float sm_scale, const adakv_output_t* out, void* ws,
+                       size_t ws_bytes, void* stream) {
+  int st;
+  if ((st = check_geometry(g)) || (st = check_q(q)) || (st = check_kv(g, kv, true)) ||
+      (st = check_out(out)))
+    return st;
+  if (!isfinite(sm_scale)) return ADAKV_ERR_VALUE;
+  if ((st = check_ws(g, 1, ws, ws_bytes))) return st;
+  return run_decode(g, q, kv, seq_lens, nullptr, 0, nullptr, nullptr, nullptr, sm_scale, out,
+                    reinterpret_cast<char*>(ws), 1, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,292 @@
+// Shared device helpers for the AdaKV gfx950 kernels: element types, 16-byte
+// vector loads, wave64 / workgroup reductions and scans.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "adakv_amd.h"
+
+namespace adakv {
+
+constexpr int kWave = 64;
+
+// ---- element types ---------------------------------------------------------
+// 16-byte vectors carry 4 fp32 or 8 fp16/bf16 elements.
+template <int DT> struct Elt;
+template <> struct Elt<ADAKV_F32> { static constexpr int kPerVec = 4; static constexpr int kBytes = 4; };
+template <> struct Elt<ADAKV_F16> { static constexpr int kPerVec = 8; static constexpr int kBytes = 2; };
+template <> struct Elt<ADAKV_BF16> { static constexpr int kPerVec = 8; static constexpr int kBytes = 2; };
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;           // NaN stays NaN
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;                  // round to nearest even
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  _Float16 x;
+  uint16_t b = (uint16_t)h;
+  __builtin_memcpy(&x, &b, 2);
+  return (float)x;
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  _Float16 x = (_Float16)f;                                       // round to nearest even
+  uint16_t b;
+  __builtin_memcpy(&b, &x, 2);
+  return b;
+}
+
+// Unpack one 16-byte vector into fp32 values.
+template <int DT>
+__device__ __forceinline__ void unpack(const uint4& v, float* out) {
+  if constexpr (DT == ADAKV_F32) {
+    out[0] = __uint_as_float(v.x); out[1] = __uint_as_float(v.y);
+    out[2] = __uint_as_float(v.z); out[3] = __uint_as_float(v.w);
+  } else {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (DT == ADAKV_BF16) {
+        out[2 * i] = __uint_as_float(w[i] << 16);
+        out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      } else {
+        out[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
+        out[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+      }
+    }
+  }
+}
+
+// Scalar load of element i of a typed array (used for q and small tails).
+__device__ __forceinline__ float load_elt(const void* p, int dt, int64_t i) {
+  if (dt == ADAKV_F32) return reinterpret_cast<const float*>(p)[i];
+  const uint16_t h = reinterpret_cast<const uint16_t*>(p)[i];
+  return dt == ADAKV_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+}
+
+__device__ __forceinline__ void store_elt(void* p, int dt, int64_t i, float x) {
+  if (dt == ADAKV_F32) {
+    reinterpret_cast<float*>(p)[i] = x;
+  } else {
+    reinterpret_cast<uint16_t*>(p)[i] =
+        (uint16_t)(dt == ADAKV_BF16 ? f32_to_bf16_bits(x) : f32_to_f16_bits(x));
+  }
+}
+
+__device__ __forceinline__ uint4 load16(const void* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+// ---- cross-lane data movement --------------------------------------------------
+// DPP moves (full-rate VALU, no LDS traffic).  Controls: quad_perm [1,0,3,2] = 0xB1,
+// quad_perm [2,3,0,1] = 0x4E, row_half_mirror = 0x141, row_mirror = 0x140.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over each aligned group of N lanes (N a power of two <= 64); every lane
+// of the group receives the group's sum.  Must be reached by all 64 lanes.
+// Values of a lane and its partner across 16-lane rows (xor 16) or wave
+// halves (xor 32), in an order that is the same for both partners; any
+// symmetric combine of the pair gives both lanes the same result.
+struct LanePair { float a, b; };
+__device__ __forceinline__ LanePair swap16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ LanePair swap32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (N >= 2) x += dpp_mov<0xB1>(x);
+  if constexpr (N >= 4) x += dpp_mov<0x4E>(x);
+  if constexpr (N >= 8) x += dpp_mov<0x141>(x);
+  if constexpr (N >= 16) x += dpp_mov<0x140>(x);
+  if constexpr (N >= 32) { const LanePair p = swap16(x); x = p.a + p.b; }
+  if constexpr (N >= 64) { const LanePair p = swap32(x); x = p.a + p.b; }
+  return x;
+}
+
+// All-lane reductions over the whole wave (every lane receives the result).
+template <typename Op>
+__device__ __forceinline__ float wave_allreduce(float x, Op op) {
+  x = op(x, dpp_mov<0xB1>(x));
+  x = op(x, dpp_mov<0x4E>(x));
+  x = op(x, dpp_mov<0x141>(x));
+  x = op(x, dpp_mov<0x140>(x));
+  LanePair p = swap16(x);
+  x = op(p.a, p.b);
+  p = swap32(x);
+  return op(p.a, p.b);
+}
+
+// ---- wave64 reductions -------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ T wave_sum(T x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ float wave_min(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fminf(x, __shfl_xor(x, o));
+  return x;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+// ---- workgroup reductions (NT threads, scratch of >= NT/64 slots) ------------
+template <int NT, typename T, typename Op>
+__device__ __forceinline__ T block_reduce(T x, T* scratch, Op op) {
+  constexpr int NW = NT / kWave;
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = op(x, __shfl_xor(x, o));
+  __syncthreads();
+  if (lane == 0) scratch[w] = x;
+  __syncthreads();
+  T r = scratch[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) r = op(r, scratch[i]);
+  return r;
+}
+
+struct OpAdd { template <typename T> __device__ T operator()(T a, T b) const { return a + b; } };
+struct OpMax { __device__ float operator()(float a, float b) const { return fmaxf(a, b); } };
+struct OpMin { __device__ float operator()(float a, float b) const { return fminf(a, b); } };
+
+// Exclusive prefix sum over the workgroup; returns this thread's offset and the total.
+template <int NT>
+__device__ __forceinline__ int block_excl_scan(int x, int* scratch, int* total) {
+  constexpr int NW = NT / kWave;
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  const int inc = wave_incl_scan(x);
+  __syncthreads();
+  if (lane == kWave - 1) scratch[w] = inc;
+  __syncthreads();
+  int base = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const int s = scratch[i];
+    base += (i < w) ? s : 0;
+    tot += s;
+  }
+  *total = tot;
+  return base + inc - x;
+}
+
+// Agent-scope publication helpers for the "last workgroup to arrive" hand-offs.
+__device__ __forceinline__ int arrive(int* counter) {
+  __threadfence();
+  return __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void reset_counter(int* counter) {
+  __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// ---- per-head block budget (adakv/budget.py:45-86, adakv/selector.py:49-52) -----
+// The bounds exactly as sparse_attention feeds them to the allocator and the
+// selector (adakv/reference.py:71-74): k_min and k_max are first clipped to nb,
+// the allocator floor is sink + local + c_min, the selector floor is the same
+// clipped to nb.
+struct BudgetCfg {
+  double avg;
+  int k_min, k_max, sink, local, c_min, policy;
+  double temperature;
+};
+
+struct Bounds {
+  int nb, sink, local, n_forced, floor_sel, lo, hi, kmin_a, kcap;
+  double target;
+};
+
+__device__ __forceinline__ Bounds budget_bounds(int nb, const BudgetCfg& p) {
+  Bounds r;
+  r.nb = nb;
+  r.kmin_a = min(p.k_min, nb);
+  r.hi = min(p.k_max, nb);
+  r.sink = min(p.sink, nb);
+  r.local = min(p.local, nb);
+  r.lo = min(max(max(r.sink + r.local + p.c_min, r.kmin_a), 1), nb);
+  r.target = fmin(fmax(p.avg, (double)r.lo), (double)r.hi);   // np.clip: hi wins when lo > hi
+  r.floor_sel = min(r.sink + r.local + p.c_min, nb);
+  r.n_forced = min(r.sink + r.local, nb);
+  // the largest count any head can receive: k <= hi for every policy, then the floor
+  r.kcap = nb <= 1 ? nb : min(max(r.hi, r.floor_sel), nb);
+  return r;
+}
+
+// Selected-block count of one head given its weight w and the sequence's sum of
+// weights (fp64, as NumPy promotes after dividing by np.log(nb)); round half to even.
+__device__ __forceinline__ int head_count(const Bounds& r, int policy, double w, double wsum, int Hq) {
+  int k;
+  if (r.nb <= 1) {
+    k = min(max(r.kmin_a, 1), r.nb);
+  } else if (policy == ADAKV_POLICY_FIXED) {
+    k = (int)rint(r.target);
+  } else {
+    const double surplus = fmax(r.target - (double)r.lo, 0.0) * (double)Hq;
+    const double x = rint((double)r.lo + surplus * w / fmax(wsum, 1e-9));
+    k = (int)fmin(fmax(x, (double)r.lo), (double)r.hi);
+  }
+  return min(max(k, r.floor_sel), r.nb);
+}
+
+// NumPy's pairwise summation of a contiguous fp64 array (8 accumulators for
+// blocks of <= 128 elements, halving above), so that the device reproduces
+// w.sum() of adakv/budget.py:84 bit for bit.
+template <int DEPTH>
+__device__ double numpy_pairwise_sum(const double* a, int n) {
+  if (n < 8) {
+    double r = 0.0;
+    for (int i = 0; i < n; ++i) r += a[i];
+    return r;
+  }
+  if (n <= 128 || DEPTH == 0) {
+    double r[8];
+    for (int j = 0; j < 8; ++j) r[j] = a[j];
+    int i = 8;
+    for (; i < n - (n % 8); i += 8)
+      for (int j = 0; j < 8; ++j) r[j] += a[i + j];
+    double res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+    for (; i < n; ++i) res += a[i];
+    return res;
+  }
+  int n2 = n / 2;
+  n2 -= n2 % 8;
+  if constexpr (DEPTH > 0)
+    return numpy_pairwise_sum<DEPTH - 1>(a, n2) + numpy_pairwise_sum<DEPTH - 1>(a + n2, n - n2);
+  return 0.0;
+}
+
+// True token count of sequence b, clamped to the capacity of the K/V views so
+// that a bad length can never move an access out of bounds.
+__device__ __forceinline__ int seq_len_of(const int32_t* seq_lens, int capacity, int b) {
+  return seq_lens ? min(max(seq_lens[b], 0), capacity) : capacity;
+}
+
+}  // namespace adakv

@@ -1,0 +1,118 @@
+// Kernel argument blocks and launcher declarations shared by the translation
+// units of libadakv_amd.so.  Host code validates every field before a launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "adakv_amd.h"
+#include "common.hpp"
+
+namespace adakv {
+
+struct CentroidArgs {
+  const void* k;
+  int64_t sb, sh, ss;          // K strides (elements)
+  void* c;                     // [B, Hkv, max_blocks, D]
+  const int32_t* seq_lens;
+  int uniform_len;
+  int B, Hkv, bs, max_blocks;
+  int n_new;                   // 0: every block; > 0: blocks holding the newest n_new tokens
+};
+
+struct ScoreArgs {
+  const void* q;
+  int qdt;
+  int64_t qsb, qsh;
+  void* c;                     // centroids (rows of appended blocks are rewritten)
+  int max_blocks;
+  const int32_t* seq_lens;
+  int uniform_len, bs;
+  int B, Hq, Hkv, G;
+  float* scores;               // [B, Hq, sp]
+  int sp;
+  // fused centroid append: recompute the blocks holding the newest n_new tokens
+  int n_new;
+  const void* k;
+  int kdt;
+  int64_t ksb, ksh, kss;
+};
+
+struct SelectArgs {
+  const float* scores;
+  int sp;
+  const int32_t* seq_lens;
+  int uniform_len, bs;
+  int B, Hq;
+  BudgetCfg cfg;
+  int32_t* table;              // [B, Hq, T]
+  int T;
+  double* wbuf;                // [B, Hq] entropy weights (adaptive policy)
+};
+
+struct BudgetArgs {
+  const double* wbuf;
+  const int32_t* seq_lens;
+  int uniform_len, bs;
+  int B, Hq;
+  BudgetCfg cfg;
+  int32_t* sel_lens;
+};
+
+struct DecodeArgs {
+  const void* q;
+  int qdt;
+  int64_t qsb, qsh;
+  const void* k;
+  const void* v;
+  int64_t sb, sh, ss;
+  const int32_t* seq_lens;
+  int uniform_len, bs;
+  int B, Hq, Hkv, G;
+  const int32_t* table;        // nullptr: dense (every block)
+  int T;
+  const int32_t* sel_lens;     // counts per head, or nullptr: derive them from wbuf / cfg
+  const double* wbuf;          // entropy weights when the counts are derived
+  BudgetCfg cfg;
+  int32_t* sel_lens_out;       // derived counts are written here (may be nullptr)
+  float scale_log2;            // sm_scale * log2(e)
+  void* out;
+  int odt;
+  int64_t osb, osh;
+  float* partials;             // [B, Hkv, nsplit, G, D + 2]
+  int nsplit;
+  int min_per;                 // fewest blocks a split takes
+  int* counters;               // [B, Hkv]
+  int max_blocks;
+  int list_cap;                // entries of the per-workgroup block list in LDS
+  int merge_in_kernel;         // 1: last split merges (sparse); 0: a merge kernel follows (dense)
+};
+
+struct MergeArgs {
+  const float* partials;
+  int nsplit;
+  int B, Hq, Hkv, G, D;
+  const int32_t* seq_lens;
+  int uniform_len, bs;
+  void* out;
+  int odt;
+  int64_t osb, osh;
+};
+
+// Workspace layout (all offsets 256-byte aligned).
+struct WorkspaceLayout {
+  size_t scores, weights, counters_plan, counters_dec, partials, table, lens, total;
+  int sp, nsplit_sparse, nsplit_dense, nsplit_max;
+};
+
+WorkspaceLayout workspace_layout(const adakv_geometry_t& g, int table_width);
+
+hipError_t launch_centroid(const CentroidArgs& a, int kdt, int cdt, int D, hipStream_t s);
+hipError_t launch_score(const ScoreArgs& a, int cdt, int D, hipStream_t s);
+hipError_t launch_select(const SelectArgs& a, int max_blocks, hipStream_t s);
+hipError_t launch_budget(const BudgetArgs& a, hipStream_t s);
+hipError_t launch_decode(const DecodeArgs& a, int kvdt, int D, hipStream_t s);
+hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
+
+}  // namespace adakv

@@ -1,0 +1,551 @@
+// Plan kernels: centroid block scores, entropy weights, top-k block selection
+// and the per-head budget (adakv/attention.py:149-247 with the numerics of the
+// NumPy oracle: adakv/estimator.py:62-74, adakv/budget.py:28-86,
+// adakv/selector.py:18-60).
+//
+// score_kernel   one workgroup per (sequence, KV head, chunk of 64 blocks).  The
+//                G query heads of the group are staged once through LDS into
+//                registers; every centroid row is read once with 16-byte loads
+//                and dotted with all G queries (fp32 FMA, then a DPP butterfly
+//                over the lanes sharing the row).  The workgroup owning the
+//                newest block(s) first recomputes their centroids from K
+//                (the decode-time append), so no separate launch is needed.
+// select_kernel  one workgroup per (sequence, q-head).  Holds the head's scores
+//                in registers, computes the normalised softmax entropy, picks
+//                the top content blocks with a linear-bin radix select plus a
+//                bitonic sort of the survivors and writes the block-table row
+//                (forced blocks, then content by descending score).  No
+//                inter-workgroup communication: the cross-head budget
+//                normalisation (budget.py:83-84) is done by its consumer.
+// budget_kernel  one workgroup per sequence: sel_lens from the weights (used
+//                by the plan-only entry point; the fused decode derives the
+//                counts itself).
+#include <float.h>
+
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace adakv {
+namespace {
+
+constexpr int kNT = 256;
+constexpr int kSortCap = 512;
+
+// N consecutive key elements of runtime type kdt starting at p (8- or 16-byte
+// aligned), widened to fp32.
+template <int N>
+__device__ __forceinline__ void load_slice(const char* p, int kdt, float* out) {
+  if (kdt == ADAKV_F32) {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) unpack<ADAKV_F32>(load16(p + 16 * i), out + 4 * i);
+  } else if constexpr (N == 8) {
+    const uint4 v = load16(p);
+    if (kdt == ADAKV_BF16) unpack<ADAKV_BF16>(v, out); else unpack<ADAKV_F16>(v, out);
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    const uint4 w = make_uint4(v.x, v.y, 0, 0);
+    float t[8];
+    if (kdt == ADAKV_BF16) unpack<ADAKV_BF16>(w, t); else unpack<ADAKV_F16>(w, t);
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = t[i];
+  }
+}
+
+__device__ __forceinline__ float round_to(float x, int dt) {
+  if (dt == ADAKV_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(x));
+  if (dt == ADAKV_F16) return f16_bits_to_f32(f32_to_f16_bits(x));
+  return x;
+}
+
+// ---------------------------------------------------------------- scores ----
+template <int CDT, int D, int GMAX>
+__global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
+  constexpr int EPV = Elt<CDT>::kPerVec;
+  constexpr int EB = Elt<CDT>::kBytes;
+  constexpr int LPR = D / EPV;              // lanes per centroid row
+  constexpr int RPL = kWave / LPR;          // rows per wave-wide load
+  constexpr int NLD = 4;                    // loads in flight per lane
+  constexpr int RPW = RPL * NLD;            // rows per wave
+  constexpr int CB = (kNT / kWave) * RPW;   // rows (blocks) per workgroup
+  __shared__ float s_q[GMAX][D];
+  __shared__ float s_sc[GMAX][CB];
+
+  const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
+  const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
+  const int row0 = chunk * CB;
+  if (row0 >= nb) return;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  const int seg = lane % LPR, rsub = lane / LPR;
+  const int G = a.G;
+
+  const int64_t cbase_el = (((int64_t)b * a.Hkv + kvh) * a.max_blocks) * D;
+  const char* cbase = reinterpret_cast<const char*>(a.c) + cbase_el * EB;
+  uint4 cv[NLD];
+  int rows[NLD];
+#pragma unroll
+  for (int i = 0; i < NLD; ++i) {
+    rows[i] = row0 + w * RPW + i * RPL + rsub;
+    cv[i] = rows[i] < nb ? load16(cbase + ((int64_t)rows[i] * D + seg * EPV) * EB)
+                         : make_uint4(0, 0, 0, 0);
+  }
+  for (int i = tid; i < G * D; i += kNT)
+    s_q[i / D][i % D] = load_elt(a.q, a.qdt, (int64_t)b * a.qsb + (int64_t)(kvh * G + i / D) * a.qsh + i % D);
+  __syncthreads();
+  float qv[GMAX][EPV];
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g)
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) qv[g][e] = g < G ? s_q[g][seg * EPV + e] : 0.f;
+
+  const int first_app = a.n_new > 0 ? max(len - a.n_new, 0) / a.bs : nb;
+#pragma unroll
+  for (int i = 0; i < NLD; ++i) {
+    float x[EPV];
+    const int r = rows[i];
+    if (r >= first_app && r < nb) {
+      // decode-time append: this block gained tokens; its centroid is the
+      // sequential fp32 mean of its real tokens, rounded once to the centroid type
+      const int t0 = r * a.bs, t1 = min(t0 + a.bs, len);
+      const int kbytes = a.kdt == ADAKV_F32 ? 4 : 2;
+      const char* kp = reinterpret_cast<const char*>(a.k) +
+                       ((int64_t)b * a.ksb + (int64_t)kvh * a.ksh + (int64_t)t0 * a.kss + seg * EPV) * kbytes;
+      const int64_t kstep = a.kss * kbytes;
+      float acc[EPV];
+      // the tokens' slices are loaded 8 at a time, then added in token order
+      for (int t = t0; t < t1; t += 8) {
+        float xs[8][EPV];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (t + u < t1) load_slice<EPV>(kp + (int64_t)(t - t0 + u) * kstep, a.kdt, xs[u]);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (t + u < t1)
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) acc[e] = t + u == t0 ? xs[u][e] : acc[e] + xs[u][e];
+      }
+      const int64_t crow = cbase_el + (int64_t)r * D + seg * EPV;
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) {
+        const float m = __fdiv_rn(acc[e], (float)(t1 - t0));
+        store_elt(a.c, CDT, crow + e, m);
+        x[e] = round_to(m, CDT);
+      }
+    } else {
+      unpack<CDT>(cv[i], x);
+    }
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      if (g < G) {
+        float p = qv[g][0] * x[0];
+#pragma unroll
+        for (int e = 1; e < EPV; ++e) p = fmaf(qv[g][e], x[e], p);
+        p = group_sum<LPR>(p);
+        if (seg == 0) s_sc[g][w * RPW + i * RPL + rsub] = p;
+      }
+    }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < G * CB; idx += kNT) {
+    const int g = idx / CB, r = idx % CB;
+    if (row0 + r < nb)
+      a.scores[((int64_t)b * a.Hq + kvh * G + g) * a.sp + row0 + r] = s_sc[g][r];
+  }
+}
+
+// ------------------------------------------------------------- selection ----
+// Order-preserving map of a (sanitised) float to uint32 plus the block index,
+// so that larger score, then smaller index, gives the larger key.
+__device__ __forceinline__ uint64_t sel_key(float x, int idx) {
+  uint32_t u = __float_as_uint(x);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint32_t)(0xffffffffu - (uint32_t)idx);
+}
+__device__ __forceinline__ int key_index(uint64_t k) {
+  return (int)(0xffffffffu - (uint32_t)(k & 0xffffffffu));
+}
+
+// NaN ranks last, infinities clamp to the finite range (they then tie with
+// +/-FLT_MAX and are ordered by block index).
+__device__ __forceinline__ float sanitize(float x) {
+  if (x != x) return -FLT_MAX;
+  return fminf(fmaxf(x, -FLT_MAX), FLT_MAX);
+}
+
+// Bitonic sort of s_keys[0, n) into descending order; n a power of two <= kSortCap.
+template <int NT>
+__device__ void bitonic_desc(uint64_t* s_keys, int n) {
+  for (int k = 2; k <= n; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < n; i += NT) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const uint64_t x = s_keys[i], y = s_keys[ixj];
+          const bool desc = (i & k) == 0;
+          if (desc ? (x < y) : (x > y)) {
+            s_keys[i] = y;
+            s_keys[ixj] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__device__ __forceinline__ int next_pow2(int n) {
+  int p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+template <int IPT>
+using MaskT = typename std::conditional<(IPT > 32), uint64_t, uint32_t>::type;
+
+template <typename M>
+__device__ __forceinline__ int popcnt(M m) {
+  if constexpr (sizeof(M) == 8) return __popcll(m); else return __popc(m);
+}
+
+// Online-softmax pair (running max, sum of exp relative to it).
+__device__ __forceinline__ void ms_merge(float& m, float& s, float m2, float s2) {
+  const float M = fmaxf(m, m2);
+  if (M == -INFINITY) { m = M; s = 0.f; return; }
+  s = s * __expf(m - M) + s2 * __expf(m2 - M);
+  m = M;
+}
+
+template <int NT, int IPT>
+__global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
+  static_assert(IPT <= 64 && IPT % 4 == 0 && NT >= 256, "one mask word per thread");
+  constexpr int NW = NT / kWave;
+  using Mask = MaskT<IPT>;
+  constexpr Mask kOne = 1;
+  __shared__ uint64_t s_keys[kSortCap];
+  __shared__ int s_hist[256];
+  __shared__ float s_r[NW][4];
+  __shared__ float s_h[NW];
+  __shared__ float s_f[NW];
+  __shared__ int s_i[NW];
+  __shared__ int s_bc[4];
+  __shared__ int s_n;
+
+  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), w = tid / kWave;
+  const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
+  const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
+  const Bounds bb = budget_bounds(nb, a.cfg);
+  const int c_lo = bb.sink, c_hi = nb - bb.local;
+  const int n_content = max(c_hi - c_lo, 0);
+  const int KC = min(max(bb.kcap - bb.n_forced, 0), n_content);
+  const bool adaptive = a.cfg.policy == ADAKV_POLICY_ADAPTIVE && nb > 1;
+  if (tid < 256) s_hist[tid] = 0;
+  if (tid == 0) s_n = 0;
+
+  // ---- forced prefix and padding of the block-table row ----
+  int32_t* trow = a.table + ((int64_t)b * a.Hq + h) * a.T;
+  const int local_lo = max(bb.sink, nb - bb.local);
+  for (int j = tid; j < bb.n_forced; j += NT) trow[j] = j < bb.sink ? j : local_lo + (j - bb.sink);
+  for (int j = bb.n_forced + KC + tid; j < a.T; j += NT) trow[j] = -1;
+
+  // ---- the head's scores: thread t owns blocks [t*IPT, (t+1)*IPT) ----
+  const float* srow = a.scores + ((int64_t)b * a.Hq + h) * a.sp;
+  const int base = tid * IPT;
+  float v[IPT];
+#pragma unroll
+  for (int i = 0; i < IPT; i += 4) {
+    if (base + i + 3 < nb) {
+      const float4 f = *reinterpret_cast<const float4*>(srow + base + i);
+      v[i] = f.x; v[i + 1] = f.y; v[i + 2] = f.z; v[i + 3] = f.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[i + j] = (base + i + j < nb) ? srow[base + i + j] : 0.f;
+    }
+  }
+
+  // ---- pass A: softmax (max, sum) of scores / T and the content score range ----
+  const float tf = (float)fmax(a.cfg.temperature, 1e-6);
+  const bool unit = tf == 1.f;
+  float m = -INFINITY, ssum = 0.f, vlo = FLT_MAX, vhi = -FLT_MAX;
+  Mask content = 0;
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int idx = base + i;
+    if (adaptive && idx < nb) {
+      const float z = unit ? v[i] : __fdiv_rn(v[i], tf);
+      if (z > m) { ssum = ssum * __expf(m - z) + 1.f; m = z; }
+      else ssum += __expf(z - m);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int idx = base + i;
+    if (idx >= c_lo && idx < c_hi) {
+      content |= kOne << i;
+      const float xs = sanitize(v[i]);
+      vlo = fminf(vlo, xs);
+      vhi = fmaxf(vhi, xs);
+    }
+  }
+  // wave reduction of the (max, sum) pairs, then min / max
+  {
+    float mm = m, ss = ssum;
+    float m2 = dpp_mov<0xB1>(mm), s2 = dpp_mov<0xB1>(ss); ms_merge(mm, ss, m2, s2);
+    m2 = dpp_mov<0x4E>(mm); s2 = dpp_mov<0x4E>(ss); ms_merge(mm, ss, m2, s2);
+    m2 = dpp_mov<0x141>(mm); s2 = dpp_mov<0x141>(ss); ms_merge(mm, ss, m2, s2);
+    m2 = dpp_mov<0x140>(mm); s2 = dpp_mov<0x140>(ss); ms_merge(mm, ss, m2, s2);
+    LanePair pm = swap16(mm), ps = swap16(ss);
+    mm = pm.a; ss = ps.a; ms_merge(mm, ss, pm.b, ps.b);
+    pm = swap32(mm); ps = swap32(ss);
+    mm = pm.a; ss = ps.a; ms_merge(mm, ss, pm.b, ps.b);
+    vlo = wave_allreduce(vlo, OpMin());
+    vhi = wave_allreduce(vhi, OpMax());
+    if (lane == 0) { s_r[w][0] = mm; s_r[w][1] = ss; s_r[w][2] = vlo; s_r[w][3] = vhi; }
+  }
+  __syncthreads();
+  m = s_r[0][0]; ssum = s_r[0][1]; vlo = s_r[0][2]; vhi = s_r[0][3];
+#pragma unroll
+  for (int ww = 1; ww < NW; ++ww) {
+    ms_merge(m, ssum, s_r[ww][0], s_r[ww][1]);
+    vlo = fminf(vlo, s_r[ww][2]);
+    vhi = fmaxf(vhi, s_r[ww][3]);
+  }
+
+  // ---- pass B: entropy terms (budget.py:33-37) and the score histogram ----
+  if (adaptive) {
+    const float inv = 1.f / ssum;
+    float hs = 0.f;
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) {
+      if (base + i < nb) {
+        const float p = __expf((unit ? v[i] : __fdiv_rn(v[i], tf)) - m) * inv;
+        hs += p * __logf(fmaxf(p, 1e-9f));
+      }
+    }
+    hs = wave_allreduce(hs, OpAdd());
+    if (lane == 0) s_h[w] = hs;
+  }
+  // 256 linear bins over [vlo, vhi]; bin 0 holds the largest scores.  The bin
+  // is a monotone function of the score, so ranks never cross bins.
+  const float width = vhi - vlo;
+  const float binv = (width > 0.f && width <= FLT_MAX) ? 256.f / width : 0.f;
+  auto bin_of = [&](float x) { return (int)fminf(255.f, floorf((vhi - x) * binv)); };
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    if ((content >> i) & kOne) {
+      v[i] = sanitize(v[i]);
+      if (KC > 0) atomicAdd(&s_hist[bin_of(v[i])], 1);
+    }
+  }
+  __syncthreads();
+  if (w == 0) {
+    if (adaptive && lane == 0) {
+      float hsum = 0.f;
+      for (int ww = 0; ww < NW; ++ww) hsum += s_h[ww];
+      a.wbuf[(int64_t)b * a.Hq + h] = (double)(-hsum) / log((double)max(nb, 2)) + 1e-6;
+    }
+    if (KC > 0) {
+      int c4[4], s4 = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { c4[j] = s_hist[4 * lane + j]; s4 += c4[j]; }
+      int before = wave_incl_scan(s4) - s4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (before < KC && KC <= before + c4[j]) { s_bc[0] = 4 * lane + j; s_bc[1] = before + c4[j]; }
+        before += c4[j];
+      }
+    }
+  }
+  __syncthreads();
+  if (KC <= 0) return;
+
+  const int bstar = s_bc[0], n_cand = s_bc[1];
+  if (n_cand <= kSortCap) {
+    // candidates: every content block in bins <= b*; rank them exactly
+#pragma unroll
+    for (int i = 0; i < IPT; ++i)
+      if (((content >> i) & kOne) && bin_of(v[i]) <= bstar) s_keys[atomicAdd(&s_n, 1)] = sel_key(v[i], base + i);
+    __syncthreads();
+    const int n = s_n;
+    for (int i = tid; i < n; i += NT) {
+      const uint64_t ki = s_keys[i];
+      int rank = 0;
+      for (int j = 0; j < n; ++j) rank += s_keys[j] > ki;
+      if (rank < KC) trow[bb.n_forced + rank] = key_index(ki);
+    }
+    return;
+  }
+
+  // ---- fallback: the boundary bin holds too many blocks; refine exactly ----
+  Mask cand = content, sel = 0;
+  int need = KC, nsel = 0;
+  bool sort_union = false;
+  for (;;) {
+    const int cnt = block_reduce<NT>(popcnt(cand), s_i, OpAdd());
+    if (need <= 0) { cand = 0; break; }
+    if (need >= cnt) { sel |= cand; cand = 0; nsel += cnt; need = 0; break; }
+    if (nsel + cnt <= kSortCap) { sort_union = true; break; }
+    if (cnt <= kSortCap) {
+      int tot;
+      const int off = block_excl_scan<NT>(popcnt(cand), s_i, &tot);
+      int o = off;
+#pragma unroll
+      for (int i = 0; i < IPT; ++i)
+        if ((cand >> i) & kOne) s_keys[o++] = sel_key(v[i], base + i);
+      const int n = next_pow2(tot);
+      for (int i = tot + tid; i < n; i += NT) s_keys[i] = 0;
+      __syncthreads();
+      bitonic_desc<NT>(s_keys, n);
+      const uint64_t kth = s_keys[need - 1];
+#pragma unroll
+      for (int i = 0; i < IPT; ++i)
+        if (((cand >> i) & kOne) && sel_key(v[i], base + i) >= kth) sel |= kOne << i;
+      nsel += need; need = 0; cand = 0;
+      __syncthreads();
+      break;
+    }
+    float lo2 = FLT_MAX, hi2 = -FLT_MAX;
+#pragma unroll
+    for (int i = 0; i < IPT; ++i)
+      if ((cand >> i) & kOne) { lo2 = fminf(lo2, v[i]); hi2 = fmaxf(hi2, v[i]); }
+    lo2 = block_reduce<NT>(lo2, s_f, OpMin());
+    hi2 = block_reduce<NT>(hi2, s_f, OpMax());
+    if (lo2 == hi2) {
+      // all candidates tie: take the lowest block indices
+      int tot;
+      const int off = block_excl_scan<NT>(popcnt(cand), s_i, &tot);
+      int r = off;
+#pragma unroll
+      for (int i = 0; i < IPT; ++i)
+        if ((cand >> i) & kOne) { if (r < need) sel |= kOne << i; ++r; }
+      nsel += need; need = 0; cand = 0;
+      break;
+    }
+    // 256 linear bins in double precision: vhi2 and vlo2 always land in
+    // different bins, so the candidate set shrinks on every pass
+    const double inv = 256.0 / ((double)hi2 - (double)lo2);
+    auto bin2 = [&](float x) { return (int)fmin(255.0, floor(((double)hi2 - (double)x) * inv)); };
+    for (int i = tid; i < 256; i += NT) s_hist[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < IPT; ++i)
+      if ((cand >> i) & kOne) atomicAdd(&s_hist[bin2(v[i])], 1);
+    __syncthreads();
+    if (tid < kWave) {
+      int c4[4], s4 = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { c4[j] = s_hist[4 * tid + j]; s4 += c4[j]; }
+      int before = wave_incl_scan(s4) - s4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (before < need && need <= before + c4[j]) { s_bc[2] = 4 * tid + j; s_bc[3] = before; }
+        before += c4[j];
+      }
+    }
+    __syncthreads();
+    const int bs2 = s_bc[2], above = s_bc[3];
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) {
+      if ((cand >> i) & kOne) {
+        const int bi = bin2(v[i]);
+        if (bi < bs2) { sel |= kOne << i; cand &= ~(kOne << i); }
+        else if (bi > bs2) cand &= ~(kOne << i);
+      }
+    }
+    nsel += above;
+    need -= above;
+    __syncthreads();
+  }
+  const Mask outm = sort_union ? (sel | cand) : sel;
+  int tot;
+  const int off = block_excl_scan<NT>(popcnt(outm), s_i, &tot);
+  if (sort_union || KC <= kSortCap) {
+    int o = off;
+#pragma unroll
+    for (int i = 0; i < IPT; ++i)
+      if ((outm >> i) & kOne) s_keys[o++] = sel_key(v[i], base + i);
+    const int n = next_pow2(tot);
+    for (int i = tot + tid; i < n; i += NT) s_keys[i] = 0;
+    __syncthreads();
+    bitonic_desc<NT>(s_keys, n);
+    for (int j = tid; j < KC; j += NT) trow[bb.n_forced + j] = key_index(s_keys[j]);
+  } else {
+    // more than kSortCap content blocks: listed in block order
+    int o = off;
+#pragma unroll
+    for (int i = 0; i < IPT; ++i)
+      if ((outm >> i) & kOne) trow[bb.n_forced + o++] = base + i;
+  }
+}
+
+// -------------------------------------------------------------- budgets ----
+__global__ __launch_bounds__(kNT) void budget_kernel(BudgetArgs a) {
+  extern __shared__ double s_w[];
+  __shared__ double s_sum;
+  const int b = blockIdx.x;
+  const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
+  const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
+  const Bounds bb = budget_bounds(nb, a.cfg);
+  const bool adaptive = a.cfg.policy == ADAKV_POLICY_ADAPTIVE && nb > 1;
+  if (adaptive) {
+    for (int h = threadIdx.x; h < a.Hq; h += kNT) s_w[h] = a.wbuf[(int64_t)b * a.Hq + h];
+    __syncthreads();
+    if (threadIdx.x == 0) s_sum = numpy_pairwise_sum<6>(s_w, a.Hq);
+    __syncthreads();
+  }
+  for (int h = threadIdx.x; h < a.Hq; h += kNT)
+    a.sel_lens[(int64_t)b * a.Hq + h] =
+        head_count(bb, a.cfg.policy, adaptive ? s_w[h] : 0.0, adaptive ? s_sum : 0.0, a.Hq);
+}
+
+template <int CDT, int D>
+hipError_t launch_score_d(const ScoreArgs& a, hipStream_t s) {
+  constexpr int EPV = Elt<CDT>::kPerVec;
+  constexpr int CB = (kNT / kWave) * (kWave / (D / EPV)) * 4;
+  dim3 grid((a.max_blocks + CB - 1) / CB, a.Hkv, a.B);
+  if (a.G <= 1) hipLaunchKernelGGL((score_kernel<CDT, D, 1>), grid, dim3(kNT), 0, s, a);
+  else if (a.G <= 2) hipLaunchKernelGGL((score_kernel<CDT, D, 2>), grid, dim3(kNT), 0, s, a);
+  else if (a.G <= 4) hipLaunchKernelGGL((score_kernel<CDT, D, 4>), grid, dim3(kNT), 0, s, a);
+  else hipLaunchKernelGGL((score_kernel<CDT, D, 8>), grid, dim3(kNT), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int CDT>
+hipError_t launch_score_c(const ScoreArgs& a, int D, hipStream_t s) {
+  switch (D) {
+    case 32: return launch_score_d<CDT, 32>(a, s);
+    case 64: return launch_score_d<CDT, 64>(a, s);
+    case 128: return launch_score_d<CDT, 128>(a, s);
+    case 256: return launch_score_d<CDT, 256>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_score(const ScoreArgs& a, int cdt, int D, hipStream_t s) {
+  switch (cdt) {
+    case ADAKV_F32: return launch_score_c<ADAKV_F32>(a, D, s);
+    case ADAKV_F16: return launch_score_c<ADAKV_F16>(a, D, s);
+    case ADAKV_BF16: return launch_score_c<ADAKV_BF16>(a, D, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_select(const SelectArgs& a, int max_blocks, hipStream_t s) {
+  dim3 grid(a.Hq, a.B);
+  if (max_blocks <= 256 * 4) hipLaunchKernelGGL((select_kernel<256, 4>), grid, dim3(256), 0, s, a);
+  else if (max_blocks <= 1024 * 4) hipLaunchKernelGGL((select_kernel<1024, 4>), grid, dim3(1024), 0, s, a);
+  else if (max_blocks <= 1024 * 8) hipLaunchKernelGGL((select_kernel<1024, 8>), grid, dim3(1024), 0, s, a);
+  else if (max_blocks <= 512 * 32) hipLaunchKernelGGL((select_kernel<512, 32>), grid, dim3(512), 0, s, a);
+  else if (max_blocks <= 512 * 64) hipLaunchKernelGGL((select_kernel<512, 64>), grid, dim3(512), 0, s, a);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_budget(const BudgetArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(budget_kernel, dim3(a.B), dim3(kNT), (size_t)a.Hq * sizeof(double), s, a);
+  return hipGetLastError();
+}
+
+}  // namespace adakv

@@ -1,0 +1,147 @@
+"""Plug AdaKV into a HuggingFace model through the attention interface
+(adakv/patch.py; transformers >= 5).
+
+    from adakv_amd.patch import patch_model
+    patch_model(model, block_size=16, avg_budget=8)   # install + enable
+    ... model.generate(...) ...
+    disable_adakv()
+
+Prefill (q_len > 1) and disabled calls go to HF's SDPA, as in the reference
+(patch.py:96-100).  Single-token decode steps run the HIP pipeline.  Unlike the
+reference, which rebuilds every centroid from the full K on every step
+(patch.py:110), each layer keeps its centroids in HBM across steps and only
+the trailing block is refreshed; batches with B > 1 are decoded sparsely when
+HF passes no attention mask (equal-length, unpadded batches), and fall back to
+SDPA otherwise.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+from .attention import instrumentation_active, record_selection
+
+try:
+    from transformers import AttentionInterface
+except Exception:  # pragma: no cover - older transformers layouts
+    from transformers.modeling_utils import AttentionInterface
+from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+_ADAKV_CFG = dict(enabled=True, block_size=16, avg_budget=16, k_min=2, k_max=64,
+                  n_sink_blocks=1, n_local_blocks=4, temperature=1.0,
+                  estimator="centroid", budget_policy="adaptive",
+                  c_min=1, nucleus_p=0.9,
+                  selection="adakv", obs_window=32, pool_kernel=7, h2o_chunk=256,
+                  centroid_dtype=None)
+_SDPA = ALL_ATTENTION_FUNCTIONS["sdpa"]
+
+
+class _LayerState:
+    """Per-layer centroids [B, Hkv, capacity_blocks, D] kept across decode steps."""
+
+    def __init__(self, key, block_size, centroid_dtype):
+        B, Hkv, S, D = key.shape
+        nb = ops.n_blocks(S, block_size)
+        cdt = centroid_dtype or (torch.float32 if key.dtype == torch.float32 else key.dtype)
+        self.sig = (B, Hkv, D, key.dtype, key.device, block_size, cdt)
+        self.centroid = torch.zeros(B, Hkv, nb + max(64, nb // 8), D, dtype=cdt, device=key.device)
+        ops.centroid_build(key, block_size, centroid=self.centroid)
+        self.seq_len = S
+
+    def grow(self, nb):
+        if nb <= self.centroid.shape[2]:
+            return
+        c = self.centroid
+        grown = torch.zeros(c.shape[0], c.shape[1], nb + max(64, nb // 8), c.shape[3], dtype=c.dtype,
+                            device=c.device)
+        grown[:, :, : c.shape[2]].copy_(c)
+        self.centroid = grown
+
+
+# Per-layer state keyed by id(module), like the reference's _FROZEN (patch.py:54).
+_STATE: dict[int, _LayerState] = {}
+
+
+def _signature(key, cfg):
+    B, Hkv, S, D = key.shape
+    cdt = cfg.get("centroid_dtype") or (torch.float32 if key.dtype == torch.float32 else key.dtype)
+    return (B, Hkv, D, key.dtype, key.device, cfg["block_size"], cdt)
+
+
+def _budget(cfg):
+    return ops.BudgetParams(avg_budget=cfg["avg_budget"], k_min=cfg["k_min"], k_max=cfg["k_max"],
+                            n_sink_blocks=cfg["n_sink_blocks"],
+                            n_local_blocks=cfg["n_local_blocks"], c_min=cfg["c_min"],
+                            temperature=cfg["temperature"], budget_policy=cfg["budget_policy"])
+
+
+def adakv_attention_forward(module, query, key, value, attention_mask, scaling, dropout=0.0,
+                            **kwargs):
+    """HF attention function (adakv/patch.py:90-121).
+
+    query [B, Hq, q_len, D], key/value [B, Hkv, S, D] -> ([B, q_len, Hq, D], None).
+    """
+    cfg = _ADAKV_CFG
+    B, Hq, q_len, D = query.shape
+    if (not cfg["enabled"]) or q_len != 1 or (B != 1 and attention_mask is not None):
+        if q_len != 1:
+            _STATE.pop(id(module), None)        # a new prefill starts a new sequence
+        return _SDPA(module, query, key, value, attention_mask=attention_mask, scaling=scaling,
+                     dropout=dropout, **kwargs)
+    if cfg.get("selection", "adakv") != "adakv":
+        raise NotImplementedError(
+            f"selection={cfg['selection']!r} (eviction baselines) is not part of the HIP path")
+    if cfg["estimator"] != "centroid":
+        if cfg["estimator"] == "minmax":
+            raise NotImplementedError("the minmax (Quest) estimator has no HIP kernel yet")
+        raise ValueError(f"unknown estimator: {cfg['estimator']!r}")
+    bs = int(cfg["block_size"])
+    S = key.shape[2]
+    st = _STATE.get(id(module))
+    if st is None or st.sig != _signature(key, cfg) or S < st.seq_len:
+        st = _LayerState(key, bs, cfg.get("centroid_dtype"))
+        _STATE[id(module)] = st
+        append_new = 0
+    else:
+        append_new = S - st.seq_len
+        st.grow(ops.n_blocks(S, bs))
+        st.seq_len = S
+    out = torch.empty(B, 1, Hq, D, dtype=query.dtype, device=query.device)
+    res = ops.decode_fused(query[:, :, 0, :], key, value, st.centroid, bs, _budget(cfg),
+                           append_new=append_new, sm_scale=scaling, out=out[:, 0],
+                           return_selection=instrumentation_active())
+    if instrumentation_active():
+        _, table, lens = res
+        record_selection(table, lens, ops.n_blocks(S, bs))
+    return out, None
+
+
+AttentionInterface.register("adakv", adakv_attention_forward)
+
+
+def install_adakv(model):
+    """Route the model's attention through "adakv" (adakv/patch.py:127-132)."""
+    try:
+        model.set_attn_implementation("adakv")
+    except Exception:  # noqa: BLE001 - older models without the setter
+        model.config._attn_implementation = "adakv"
+    return model
+
+
+def enable_adakv(**cfg):
+    """Update the configuration and enable the sparse decode (adakv/patch.py:135-138)."""
+    _ADAKV_CFG.update(cfg)
+    _ADAKV_CFG["enabled"] = True
+    _STATE.clear()
+
+
+def disable_adakv():
+    _ADAKV_CFG["enabled"] = False
+
+
+def patch_model(model, **cfg):
+    """install_adakv + enable_adakv in one call (the README entry point,
+    README.md:12-15, which the reference advertises but does not define)."""
+    install_adakv(model)
+    enable_adakv(**cfg)
+    return model

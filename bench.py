@@ -1,0 +1,262 @@
+#!/usr/bin/env python3
+"""AdaKV decode-attention benchmark on one MI355X.
+
+Workload (N=1): one Llama-3.1-8B-shaped attention layer
+decoding one token -- batch 1, 32 q / 8 KV heads, head_dim 128, context
+131072, bf16 K/V ~ N(0,1), block_size 16, avg_budget 8 (adaptive entropy
+budget, sink 1, local 4, c_min 1, k_max 64).  Every KV head holds 4 planted
+"needle" blocks whose keys are 3 * q + noise for one of its q-heads.
+
+A step is one layer's full decode-attention op: centroid append for the new
+token, block scores, budget + selection, sparse split-K decode and merge
+(adakv_decode_fused).  Steps cycle over ``--layers`` independent layers'
+K/V/centroid buffers (32 by default: 16 GiB of K/V, 512 MiB of centroids,
+more than the 256 MB MALL) so every step reads HBM.  Launches are captured in
+a HIP graph (one graph = one pass over the layers) to take host overhead out.
+
+Prints one JSON line: value = microseconds per layer (lower is better), the
+achieved HBM GB/s on the algorithmic bytes of the op, the dense HIP
+flash-decode time at the same context, the roofline of the dominant kernel
+(the centroid scan) timed with HIP events, and the CPU oracle timed on one
+layer of the same workload on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+PEAK_HBM_GBPS = 8000.0
+METRIC = "decode attn µs/layer @128K + achieved HBM GB/s (KV bytes touched), 1 MI355X"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=640, help="timed layer-steps (rounded up to a multiple of --layers)")
+    ap.add_argument("--warmup", type=int, default=64, help="untimed layer-steps")
+    ap.add_argument("--ctx", type=int, default=131072)
+    ap.add_argument("--avg-budget", type=float, default=8)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU-oracle time budget")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--seed", type=int, default=0)
+    return ap.parse_args()
+
+
+class Workload:
+    Hq, Hkv, D, BS = 32, 8, 128, 16
+
+    def __init__(self, torch, ops, ctx, layers, avg_budget, seed):
+        self.torch, self.ops = torch, ops
+        self.S, self.L = ctx, layers
+        self.nb = ops.n_blocks(ctx, self.BS)
+        self.budget = ops.BudgetParams(avg_budget=avg_budget)
+        dev = torch.device("cuda:0")
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        G = self.Hq // self.Hkv
+        self.q, self.k, self.v, self.c, self.out, self.needles = [], [], [], [], [], []
+        rng = torch.Generator().manual_seed(seed)
+        for _ in range(layers):
+            q = torch.randn(1, self.Hq, self.D, device=dev, dtype=torch.bfloat16, generator=gen)
+            k = torch.randn(1, self.Hkv, ctx, self.D, device=dev, dtype=torch.bfloat16, generator=gen)
+            v = torch.randn(1, self.Hkv, ctx, self.D, device=dev, dtype=torch.bfloat16, generator=gen)
+            # 4 needle blocks per KV head at content positions (not sink, not local)
+            pos = torch.randint(1, self.nb - 4, (self.Hkv, 4), generator=rng)
+            for g in range(self.Hkv):
+                for j in range(4):
+                    b = int(pos[g, j])
+                    lo, hi = b * self.BS, min((b + 1) * self.BS, ctx)
+                    k[0, g, lo:hi] = (3.0 * q[0, g * G + j].float()[None, :] +
+                                      torch.randn(hi - lo, self.D, device=dev, generator=gen)).to(torch.bfloat16)
+            c = ops.centroid_build(k, self.BS)
+            self.q.append(q)
+            self.k.append(k)
+            self.v.append(v)
+            self.c.append(c)
+            self.out.append(torch.empty(1, self.Hq, self.D, device=dev, dtype=torch.bfloat16))
+            self.needles.append(pos)
+        torch.cuda.synchronize()
+
+    def step(self, l):
+        self.ops.decode_fused(self.q[l], self.k[l], self.v[l], self.c[l], self.BS, self.budget,
+                              append_new=1, out=self.out[l])
+
+    def dense(self, l):
+        self.ops.dense_decode(self.q[l], self.k[l], self.v[l], out=self.out[l])
+
+    def scores(self, l, buf):
+        self.ops.block_scores(self.q[l], self.c[l], self.BS, seq_len=self.S, out=buf)
+
+
+def capture(torch, fn, layers, stream):
+    """One HIP graph holding fn(0..layers-1), after a warm pass on the capture stream."""
+    with torch.cuda.stream(stream):
+        for l in range(layers):
+            fn(l)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for l in range(layers):
+            fn(l)
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, replays, warm):
+    """HIP-event time of `replays` graph replays on the current stream (ms)."""
+    for _ in range(warm):
+        g.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    s.record()
+    for _ in range(replays):
+        g.replay()
+    e.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    return s.elapsed_time(e), wall
+
+
+def selection_bytes(torch, ops, w: Workload):
+    """Algorithmic bytes of one layer step, from the actual selection of every layer."""
+    e = 2
+    uniq = []
+    for l in range(w.L):
+        _, table, lens = ops.decode_fused(w.q[l], w.k[l], w.v[l], w.c[l], w.BS, w.budget,
+                                          return_selection=True)
+        t, n = table[0].cpu(), lens[0].cpu()
+        G = w.Hq // w.Hkv
+        u = 0
+        for g in range(w.Hkv):
+            s = set()
+            for h in range(g * G, (g + 1) * G):
+                s.update(t[h, : int(n[h])].tolist())
+            u += len(s)
+        uniq.append(u)
+    u = sum(uniq) / len(uniq)
+    T = ops.table_width(1, w.Hq, w.Hkv, w.D, w.BS, w.S, w.c[0].shape[2], w.budget)
+    b_cent = w.Hkv * w.nb * w.D * e
+    b_kv = u * w.BS * w.D * e * 2
+    b_q = b_out = w.Hq * w.D * e
+    b_meta = w.Hq * T * 4 * 2 + w.Hq * 4 * 2 + w.Hkv * (w.BS * w.D * e + w.D * e)
+    return dict(centroid=b_cent, kv=b_kv, q=b_q, out=b_out, meta=b_meta,
+                total=b_cent + b_kv + b_q + b_out + b_meta, union_blocks_per_layer=u)
+
+
+def cpu_baseline(torch, w: Workload, budget_s: float):
+    """The NumPy oracle (reference.sparse_attention restated) on layer 0 of the
+    same workload, single-threaded NumPy einsum; median seconds per layer."""
+    import numpy as np
+
+    from oracle import adakv_oracle as O
+    q = w.q[0][0].float().cpu().numpy()
+    K = O.expand_gqa(w.k[0][0].float().cpu().numpy(), w.Hq)
+    V = O.expand_gqa(w.v[0][0].float().cpu().numpy(), w.Hq)
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        O.sparse_attention(q, K, V, block_size=w.BS, avg_budget=w.budget.avg_budget)
+        times.append(time.perf_counter() - t0)
+        log(f"cpu oracle run {len(times)}: {times[-1]:.2f}s")
+        if len(times) >= 5 or time.perf_counter() - t_start + times[-1] > budget_s:
+            break
+    del K, V
+    runs = times[1:] if len(times) > 1 else times
+    return float(np.median(runs)), len(times)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one MI355X; multi-GPU runs are not part of it "
+              "(see DESIGN.md for how the path would shard)", file=sys.stderr)
+        sys.exit(2)
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import torch
+
+    from adakv_amd import _capi, ops
+    _capi.load()
+    assert torch.cuda.is_available(), "bench.py needs a ROCm device"
+    log(f"device {torch.cuda.get_device_name(0)}; building {args.layers} layers at ctx {args.ctx}")
+    w = Workload(torch, ops, args.ctx, args.layers, args.avg_budget, args.seed)
+    L = w.L
+    replays = max(1, math.ceil(args.steps / L))
+    warm = max(1, math.ceil(args.warmup / L))
+    steps = replays * L
+    stream = torch.cuda.Stream()
+
+    log("capturing the decode graph")
+    g_step = capture(torch, w.step, L, stream)
+    ms, wall = time_graph(torch, g_step, replays, warm)
+    us_layer = ms * 1e3 / steps
+    log(f"adakv fused: {us_layer:.2f} us/layer (events), wall {wall * 1e3 / steps:.2f} us/layer")
+
+    nbytes = selection_bytes(torch, ops, w)
+    gbps = nbytes["total"] / (us_layer * 1e-6) / 1e9
+
+    # dominant kernel: the centroid scan, alone, over the same rotated layers
+    sbuf = torch.zeros(1, w.Hq, w.c[0].shape[2], device="cuda", dtype=torch.float32)
+    g_sc = capture(torch, lambda l: w.scores(l, sbuf), L, stream)
+    ms_sc, _ = time_graph(torch, g_sc, replays, warm)
+    us_sc = ms_sc * 1e3 / steps
+    sc_bytes = nbytes["centroid"] + nbytes["q"]
+    sc_gbps = sc_bytes / (us_sc * 1e-6) / 1e9
+    log(f"centroid scan: {us_sc:.2f} us/launch, {sc_gbps:.0f} GB/s")
+
+    dense_us = None
+    if not args.no_dense:
+        g_d = capture(torch, w.dense, L, stream)
+        ms_d, _ = time_graph(torch, g_d, max(1, replays // 8), 1)
+        dense_us = ms_d * 1e3 / (max(1, replays // 8) * L)
+        dense_gbps = (2 * w.Hkv * w.S * w.D * 2) / (dense_us * 1e-6) / 1e9
+        log(f"dense flash-decode: {dense_us:.1f} us/layer ({dense_gbps:.0f} GB/s)")
+
+    cpu = None
+    if not args.no_cpu:
+        sec, runs = cpu_baseline(torch, w, args.cpu_seconds)
+        cpu = {"value": round(sec * 1e6, 1), "unit": "us/layer", "cores": 1, "kind": "port",
+               "sample": f"oracle.sparse_attention on layer 0 of this workload (ctx {w.S}, "
+                         f"32/8 heads, fp32 NumPy, GQA-expanded K/V), {runs} runs, median of "
+                         f"runs after the first; host has {os.cpu_count()} CPUs, "
+                         f"{len(os.sched_getaffinity(0))} in affinity, NumPy einsum single-threaded"}
+        log(f"cpu oracle: {sec:.2f} s/layer")
+
+    res = {
+        "metric": METRIC, "value": round(us_layer, 3), "unit": "us/layer", "n_gpus": 1,
+        "steps": steps, "warmup": warm * L, "ms_per_step": round(us_layer / 1e3, 6),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "llama3.1-8b attention layer decode, ctx 131072, avg_budget 8 (BASELINE config 3)",
+                   "batch": 1, "n_q_heads": w.Hq, "n_kv_heads": w.Hkv, "head_dim": w.D,
+                   "context": w.S, "block_size": w.BS, "avg_budget": args.avg_budget,
+                   "layers_rotated": L},
+        "achieved_GBps": round(gbps, 1),
+        "bytes_per_layer": int(nbytes["total"]),
+        "kv_bytes_per_layer": int(nbytes["kv"]),
+        "union_blocks_per_layer": round(nbytes["union_blocks_per_layer"], 2),
+        "roofline_frac_whole_op": round(gbps / PEAK_HBM_GBPS, 4),
+        "dense_us_per_layer": None if dense_us is None else round(dense_us, 2),
+        "speedup_vs_dense": None if dense_us is None else round(dense_us / us_layer, 2),
+        "roofline": {"kernel": "score_kernel (centroid scan)", "bound": "hbm",
+                     "achieved": round(sc_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(sc_gbps / PEAK_HBM_GBPS, 4), "traffic": None,
+                     "launch_us": round(us_sc, 3), "bytes_per_launch": int(sc_bytes)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,179 @@
+/*
+ * adakv_amd.h -- C ABI of the MI355X (gfx950) AdaKV decode hot path.
+ *
+ * Plain C: device pointers, sizes, strides and a HIP stream passed as void*.
+ * No call allocates device memory or synchronises the host; every launch is
+ * ordered on the given stream (NULL = the default stream).  Scratch memory is
+ * a caller-owned workspace sized by adakv_workspace_bytes().  Its first 64 KiB
+ * hold hand-off counters: zero-fill them once before the first use; every
+ * call leaves them zeroed again, whatever the geometry of the next call.
+ * Calls that share a workspace must not overlap (use one workspace per stream).
+ *
+ * Layouts (element strides; head_dim is always the contiguous axis):
+ *   query    [batch, n_q_heads, head_dim]
+ *   K, V     [batch, n_kv_heads, max_seq_len, head_dim]   (one stride set for both)
+ *   centroid [batch, n_kv_heads, max_blocks, head_dim]    (contiguous)
+ *   table    [batch, n_q_heads, table_width] int32, sel_lens [batch, n_q_heads] int32
+ *   output   [batch, n_q_heads, head_dim]
+ * seq_lens is a device int32 array [batch] of true token counts, or NULL when
+ * every sequence holds max_seq_len tokens.  q-head h reads KV head
+ * h / (n_q_heads / n_kv_heads) (grouped-query attention).
+ *
+ * Reference interfaces replaced (liukefan821/adakv):
+ *   adakv_centroid_build   <- AdaKVCache.append_prefill          adakv/attention.py:119-139
+ *                             build_block_summaries("centroid")  adakv/estimator.py:27-48
+ *   adakv_centroid_append  <- update_cache_decode                adakv/runtime.py:43-60
+ *                             (and the TODO AdaKVCache.append_decode, adakv/attention.py:141-146)
+ *   adakv_block_scores     <- block_scores("centroid")           adakv/estimator.py:62-74
+ *   adakv_plan             <- plan_selection                     adakv/attention.py:149-247
+ *                             (estimator.py:62-74, budget.py:45-86, selector.py:18-60)
+ *   adakv_sparse_decode    <- block_sparse_decode                adakv/kernels/block_sparse_decode.py:103-135
+ *   adakv_decode_fused     <- adakv_decode_attention             adakv/attention.py:250-268
+ *                             adakv_decode_step                  adakv/runtime.py:85-112
+ *   adakv_dense_decode     <- dense_decode                       benchmarks/efficiency/bench_decode_latency.py:40-53
+ */
+#ifndef ADAKV_AMD_H
+#define ADAKV_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ADAKV_ABI_VERSION 1
+
+/* Status codes.  Argument errors are detected on the host before any launch. */
+enum {
+  ADAKV_OK = 0,
+  ADAKV_ERR_NULL = 1,         /* a required pointer is NULL                        */
+  ADAKV_ERR_SHAPE = 2,        /* inconsistent sizes (e.g. n_q_heads % n_kv_heads)  */
+  ADAKV_ERR_DTYPE = 3,        /* unsupported or mismatched element type            */
+  ADAKV_ERR_UNSUPPORTED = 4,  /* valid but not built: head_dim, group, max_blocks  */
+  ADAKV_ERR_WORKSPACE = 5,    /* workspace too small or not 256-byte aligned       */
+  ADAKV_ERR_LAUNCH = 6,       /* the HIP runtime reported a launch error           */
+  ADAKV_ERR_VALUE = 7         /* bad parameter value (budget, policy, alignment)   */
+};
+
+enum { ADAKV_F32 = 0, ADAKV_F16 = 1, ADAKV_BF16 = 2 };
+
+/* Budget policies (adakv/budget.py:45-86).  "adaptive_nucleus" is not built. */
+enum { ADAKV_POLICY_FIXED = 0, ADAKV_POLICY_ADAPTIVE = 1 };
+
+typedef struct {
+  int32_t batch;        /* sequences in the batch (<= 4096, batch*n_kv_heads <= 12288) */
+  int32_t n_q_heads;
+  int32_t n_kv_heads;   /* n_q_heads / n_kv_heads <= 8                             */
+  int32_t head_dim;     /* 32, 64, 128 or 256                                      */
+  int32_t block_size;   /* tokens per KV block, 1..256                             */
+  int32_t max_seq_len;  /* token capacity of the K/V views                         */
+  int32_t max_blocks;   /* centroid rows per (sequence, KV head); >= ceil(max_seq_len/block_size), <= 32768 */
+} adakv_geometry_t;
+
+typedef struct {        /* query [batch, n_q_heads, head_dim] */
+  const void* data;
+  int32_t dtype;
+  int64_t stride_b, stride_h;
+} adakv_query_t;
+
+typedef struct {        /* output [batch, n_q_heads, head_dim] */
+  void* data;
+  int32_t dtype;
+  int64_t stride_b, stride_h;
+} adakv_output_t;
+
+typedef struct {        /* K and V caches [batch, n_kv_heads, max_seq_len, head_dim] */
+  const void* k;
+  const void* v;
+  int32_t dtype;        /* same element type for K and V                           */
+  int64_t stride_b, stride_h, stride_s;
+} adakv_kv_t;
+
+typedef struct {        /* centroids [batch, n_kv_heads, max_blocks, head_dim], contiguous */
+  void* data;
+  int32_t dtype;        /* ADAKV_F32 (exact selection parity) or ADAKV_BF16 / ADAKV_F16 */
+} adakv_centroid_t;
+
+typedef struct {        /* plan_selection keyword arguments (adakv/attention.py:149-162) */
+  double avg_budget;
+  int32_t k_min, k_max;
+  int32_t n_sink_blocks, n_local_blocks, c_min;
+  double temperature;
+  int32_t policy;
+} adakv_budget_t;
+
+typedef struct {        /* block_table [batch, n_q_heads, table_width], sel_lens [batch, n_q_heads] */
+  int32_t* block_table;
+  int32_t table_width;
+  int32_t* sel_lens;
+} adakv_selection_t;
+
+const char* adakv_status_string(int status);
+int adakv_abi_version(void);
+
+/* Width of the block table a plan writes: the largest per-head count any
+ * sequence can receive, max(1, min(max(k_max, sink+local+c_min), max_blocks)).
+ * The reference returns width max(sel_lens) after a device->host sync
+ * (adakv/attention.py:242); this ABI never syncs and uses the static bound. */
+int32_t adakv_table_width(const adakv_geometry_t* g, const adakv_budget_t* p);
+
+/* Workspace bytes for plan / decode / fused / dense calls on this geometry. */
+size_t adakv_workspace_bytes(const adakv_geometry_t* g, int32_t table_width);
+
+/* Mean key of every block over its real tokens (sequential fp32 sum / count),
+ * stored in the centroid dtype.  adakv/estimator.py:27-48, adakv/attention.py:119-139. */
+int adakv_centroid_build(const adakv_geometry_t* g, const adakv_kv_t* kv, const int32_t* seq_lens,
+                         const adakv_centroid_t* centroid, void* stream);
+
+/* After n_new tokens were written at positions [len-n_new, len) of every
+ * sequence, recompute the centroids of the blocks holding them (O(block_size*D)
+ * per KV head; identical bits to a full rebuild).  adakv/runtime.py:43-60. */
+int adakv_centroid_append(const adakv_geometry_t* g, const adakv_kv_t* kv, const int32_t* seq_lens,
+                          int32_t n_new, const adakv_centroid_t* centroid, void* stream);
+
+/* Block scores q . centroid for every (sequence, q-head, block), fp32, no
+ * 1/sqrt(D) (adakv/estimator.py:62-74).  scores [batch, n_q_heads, pitch] with
+ * pitch >= max_blocks; entries past a sequence's last block are left untouched. */
+int adakv_block_scores(const adakv_geometry_t* g, const adakv_query_t* q,
+                       const adakv_centroid_t* centroid, const int32_t* seq_lens, float* scores,
+                       int32_t pitch, void* stream);
+
+/* Score every block by q . centroid, split the mean-pinned budget across the
+ * heads of each sequence, select sink + local + top-scoring blocks.
+ * Rows list forced blocks (ascending) then content blocks by descending score
+ * (ties: lower block id first); entries past sel_lens are never read (further
+ * ranked candidates, then -1).  adakv/attention.py:149-247. */
+int adakv_plan(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_centroid_t* centroid,
+               const int32_t* seq_lens, const adakv_budget_t* budget, const adakv_selection_t* sel,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* Attention of each q-head over exactly the tokens of its listed blocks
+ * (duplicates and out-of-range ids ignored, tokens >= seq_len masked), fp32
+ * accumulation, output in out->dtype.  Each KV block selected by several heads
+ * of a group is read once.  adakv/kernels/block_sparse_decode.py:103-135. */
+int adakv_sparse_decode(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
+                        const int32_t* seq_lens, const adakv_selection_t* sel, float sm_scale,
+                        const adakv_output_t* out, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* One decode step: optional centroid append of the newest append_new tokens,
+ * plan, sparse decode.  sel may be NULL (selection kept in the workspace) or
+ * name caller buffers that receive the selection.  adakv/attention.py:250-268. */
+int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
+                       const adakv_centroid_t* centroid, const int32_t* seq_lens,
+                       const adakv_budget_t* budget, const adakv_selection_t* sel,
+                       int32_t append_new, float sm_scale, const adakv_output_t* out,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* Dense split-K flash-decode over every token (the comparison baseline).
+ * benchmarks/efficiency/bench_decode_latency.py:40-53. */
+int adakv_dense_decode(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
+                       const int32_t* seq_lens, float sm_scale, const adakv_output_t* out,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ADAKV_AMD_H */

@@ -1,0 +1,171 @@
+"""The C-ABI library on a CPU-only host: it loads, exports every symbol the
+header declares, and rejects bad arguments on the host with the documented
+status codes before touching a device."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from adakv_amd import _capi as C
+from adakv_amd import ops
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "adakv_amd.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(C.lib_path()):
+        pytest.skip("libadakv_amd.so not built (run python -m adakv_amd.build)")
+    return C.load()
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(adakv_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_entry_points():
+    names = _declared()
+    for n in ("adakv_centroid_build", "adakv_centroid_append", "adakv_plan", "adakv_sparse_decode",
+              "adakv_decode_fused", "adakv_dense_decode", "adakv_workspace_bytes",
+              "adakv_table_width"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for n in _declared():
+        assert hasattr(lib, n), n
+        assert n in C.SIGNATURES, f"{n} has no ctypes signature"
+
+
+def test_abi_version_and_status_strings(lib):
+    assert lib.adakv_abi_version() == C.ABI_VERSION
+    for s in range(8):
+        assert lib.adakv_status_string(s)
+    assert lib.adakv_status_string(99) == b"unknown status"
+
+
+def _g(**kw):
+    d = dict(B=1, Hq=32, Hkv=8, D=128, block_size=16, max_seq_len=131072, max_blocks=8192)
+    d.update(kw)
+    return C.Geometry(d["B"], d["Hq"], d["Hkv"], d["D"], d["block_size"], d["max_seq_len"],
+                      d["max_blocks"])
+
+
+def _b(**kw):
+    return ops.BudgetParams(**kw).to_c()
+
+
+def test_table_width_is_the_static_bound(lib):
+    g = _g()
+    assert lib.adakv_table_width(ctypes.byref(g), ctypes.byref(_b(avg_budget=8))) == 64
+    assert lib.adakv_table_width(ctypes.byref(g), ctypes.byref(_b(k_max=2))) == 6   # sink+local+c_min
+    assert lib.adakv_table_width(ctypes.byref(g), ctypes.byref(_b(k_max=100000))) == 8192
+    small = _g(max_seq_len=40, max_blocks=3)
+    assert lib.adakv_table_width(ctypes.byref(small), ctypes.byref(_b())) == 3
+
+
+@pytest.mark.parametrize("bad,code", [
+    (dict(Hq=30, Hkv=8), C.ADAKV_ERR_SHAPE),
+    (dict(Hq=72, Hkv=8), C.ADAKV_ERR_UNSUPPORTED),       # group 9 > 8
+    (dict(D=96), C.ADAKV_ERR_UNSUPPORTED),
+    (dict(max_blocks=100), C.ADAKV_ERR_SHAPE),           # too few blocks for max_seq_len
+    (dict(max_seq_len=65536 * 16, max_blocks=65536), C.ADAKV_ERR_UNSUPPORTED),
+    (dict(B=0), C.ADAKV_ERR_SHAPE),
+])
+def test_geometry_validation(lib, bad, code):
+    g = _g(**bad)
+    q = C.Query(0x1000, C.ADAKV_BF16, 4096, 128)
+    assert lib.adakv_dense_decode(ctypes.byref(g), ctypes.byref(q), None, None, ctypes.c_float(1.0),
+                                  None, None, 0, None) == code
+    assert lib.adakv_workspace_bytes(ctypes.byref(g), 64) == 0
+
+
+def test_null_and_dtype_validation(lib):
+    g = _g()
+    kv = C.KV(0x1000, 0x2000, C.ADAKV_BF16, 0, 131072 * 128, 128)
+    q = C.Query(0x1000, C.ADAKV_BF16, 4096, 128)
+    out = C.Output(0x3000, C.ADAKV_BF16, 4096, 128)
+    ws = ctypes.c_void_p(0x10000)
+    f = lib.adakv_dense_decode
+    assert f(ctypes.byref(g), None, ctypes.byref(kv), None, ctypes.c_float(1.0), ctypes.byref(out), ws,
+             1 << 30, None) == C.ADAKV_ERR_NULL
+    bad_q = C.Query(0x1000, 7, 4096, 128)
+    assert f(ctypes.byref(g), ctypes.byref(bad_q), ctypes.byref(kv), None, ctypes.c_float(1.0),
+             ctypes.byref(out), ws, 1 << 30, None) == C.ADAKV_ERR_DTYPE
+    misaligned = C.KV(0x1002, 0x2000, C.ADAKV_BF16, 0, 131072 * 128, 128)
+    assert f(ctypes.byref(g), ctypes.byref(q), ctypes.byref(misaligned), None, ctypes.c_float(1.0),
+             ctypes.byref(out), ws, 1 << 30, None) == C.ADAKV_ERR_VALUE
+    assert f(ctypes.byref(g), ctypes.byref(q), ctypes.byref(kv), None, ctypes.c_float(1.0),
+             ctypes.byref(out), ws, 16, None) == C.ADAKV_ERR_WORKSPACE
+    assert f(ctypes.byref(g), ctypes.byref(q), ctypes.byref(kv), None, ctypes.c_float(1.0),
+             ctypes.byref(out), ctypes.c_void_p(0x10010), 1 << 30, None) == C.ADAKV_ERR_WORKSPACE
+    assert f(ctypes.byref(g), ctypes.byref(q), ctypes.byref(kv), None, ctypes.c_float(float("nan")),
+             ctypes.byref(out), ws, 1 << 30, None) == C.ADAKV_ERR_VALUE
+
+
+def test_plan_validation(lib):
+    g = _g()
+    q = C.Query(0x1000, C.ADAKV_BF16, 4096, 128)
+    c = C.Centroid(0x4000, C.ADAKV_BF16)
+    ws = ctypes.c_void_p(0x10000)
+    sel = C.Selection(0x5000, 64, 0x6000)
+    narrow = C.Selection(0x5000, 8, 0x6000)
+    bad_policy = C.Budget(8.0, 2, 64, 1, 4, 1, 1.0, 5)
+    neg = C.Budget(8.0, 2, -1, 1, 4, 1, 1.0, 1)
+    ok = _b(avg_budget=8)
+    f = lib.adakv_plan
+    args = lambda b, s: (ctypes.byref(g), ctypes.byref(q), ctypes.byref(c), None, ctypes.byref(b),
+                         ctypes.byref(s), ws, 1 << 30, None)
+    assert f(*args(bad_policy, sel)) == C.ADAKV_ERR_VALUE
+    assert f(*args(neg, sel)) == C.ADAKV_ERR_VALUE
+    assert f(*args(ok, narrow)) == C.ADAKV_ERR_SHAPE
+    nullsel = C.Selection(0, 64, 0x6000)
+    assert f(*args(ok, nullsel)) == C.ADAKV_ERR_NULL
+
+
+def test_centroid_dtype_pairs(lib):
+    g = _g()
+    kv = C.KV(0x1000, 0, C.ADAKV_F16, 0, 131072 * 128, 128)
+    c = C.Centroid(0x4000, C.ADAKV_BF16)
+    assert lib.adakv_centroid_build(ctypes.byref(g), ctypes.byref(kv), None, ctypes.byref(c),
+                                    None) == C.ADAKV_ERR_DTYPE
+    c2 = C.Centroid(0x4000, C.ADAKV_F16)
+    assert lib.adakv_centroid_append(ctypes.byref(g), ctypes.byref(kv), None, 0, ctypes.byref(c2),
+                                     None) == C.ADAKV_ERR_VALUE          # n_new must be >= 1
+
+
+def test_workspace_bytes_grows_with_the_problem(lib):
+    small, big = _g(max_seq_len=4096, max_blocks=256), _g()
+    assert 0 < lib.adakv_workspace_bytes(ctypes.byref(small), 64) < \
+        lib.adakv_workspace_bytes(ctypes.byref(big), 64)
+    assert lib.adakv_workspace_bytes(ctypes.byref(big), 0) == 0
+
+
+def test_python_errors_mirror_the_reference(lib):
+    """Unknown estimator / policy -> ValueError; CPU tensors -> RuntimeError
+    (the reference raises RuntimeError without its GPU kernel)."""
+    import torch
+
+    from adakv_amd.attention import AdaKVCache, plan_selection
+    from adakv_amd.kernels.block_sparse_decode import block_sparse_decode
+    with pytest.raises(ValueError):
+        AdaKVCache(16, estimator="bogus")
+    cache = AdaKVCache(16)
+    with pytest.raises(RuntimeError):
+        cache.append_prefill(torch.zeros(2, 64, 32), torch.zeros(2, 64, 32))
+    with pytest.raises(ValueError):
+        plan_selection(torch.zeros(4, 32), cache, 8, estimator="nope")
+    with pytest.raises(ValueError):
+        plan_selection(torch.zeros(4, 32), cache, 8, budget_policy="nope")
+    with pytest.raises(ValueError):
+        plan_selection(torch.zeros(4, 32), cache, 8, estimator="minmax")
+    with pytest.raises(NotImplementedError):
+        ops.BudgetParams(budget_policy="adaptive_nucleus").to_c()
+    with pytest.raises(RuntimeError):
+        block_sparse_decode(torch.zeros(4, 32), torch.zeros(2, 64, 32), torch.zeros(2, 64, 32),
+                            torch.zeros(4, 2, dtype=torch.int32), torch.ones(4, dtype=torch.int32), 16)
