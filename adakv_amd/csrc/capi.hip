@@ -121,12 +121,11 @@ int list_cap_of(const adakv_geometry_t& g, int T, int nsplit) {
                                                      std::min<int64_t>(kSparseMinPer, umax)));
 }
 
-// LDS of the decode kernel: static arrays (sized for 8 waves) plus, in sparse
-// mode, the weights, the union bitmap and the block list.
-size_t decode_lds_bytes(const adakv_geometry_t& g, int list_cap, bool sparse) {
-  const int GM = gmax_of(g.n_q_heads / g.n_kv_heads), D = g.head_dim, NW = 8;
-  const int hc = std::max(1, std::min(GM, 8192 / (NW * D)));
-  const size_t stat = (size_t)GM * D * 4 + (size_t)NW * hc * D * 4 + (size_t)2 * NW * GM * 4 + 256;
+// LDS of the decode kernel: its static arrays plus, in sparse mode, the
+// weights, the union bitmap and the block list.
+size_t decode_lds_bytes(const adakv_geometry_t& g, int kvdt, int list_cap, bool sparse) {
+  const int GM = gmax_of(g.n_q_heads / g.n_kv_heads);
+  const size_t stat = decode_static_lds(kvdt, g.head_dim, GM, sparse);
   const size_t dyn = sparse ? ((size_t)g.n_q_heads * 8 + 15) / 16 * 16 +
                                   (size_t)(((g.max_blocks + 3) / 4) + list_cap) * 4
                             : 16;
@@ -234,7 +233,7 @@ int run_decode(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv
     d.list_cap = 0;
     d.merge_in_kernel = 0;
   }
-  if (decode_lds_bytes(*g, d.list_cap, table != nullptr) > kLdsLimit) return ADAKV_ERR_UNSUPPORTED;
+  if (decode_lds_bytes(*g, kv->dtype, d.list_cap, table != nullptr) > kLdsLimit) return ADAKV_ERR_UNSUPPORTED;
   if (launch_decode(d, kv->dtype, g->head_dim, s) != hipSuccess) return ADAKV_ERR_LAUNCH;
   if (table) return ADAKV_OK;
   MergeArgs m{};

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "adakv_amd.h"
 
 namespace adakv {
@@ -59,6 +61,49 @@ __device__ __forceinline__ void unpack(const uint4& v, float* out) {
       }
     }
   }
+}
+
+// Element i of an array of compile-time type DT, widened to fp32.
+template <int DT>
+__device__ __forceinline__ float load_t(const void* p, int64_t i) {
+  if constexpr (DT == ADAKV_F32) {
+    return reinterpret_cast<const float*>(p)[i];
+  } else {
+    const uint16_t h = reinterpret_cast<const uint16_t*>(p)[i];
+    if constexpr (DT == ADAKV_BF16) return bf16_bits_to_f32(h); else return f16_bits_to_f32(h);
+  }
+}
+
+// Calls f(std::integral_constant<int, DT>) for the runtime dtype dt, so that
+// the loads inside f are typed at compile time (a runtime type test between
+// loads makes the compiler wait for each load before issuing the next).
+template <typename F>
+__device__ __forceinline__ void with_dtype(int dt, F&& f) {
+  if (dt == ADAKV_BF16) f(std::integral_constant<int, ADAKV_BF16>{});
+  else if (dt == ADAKV_F16) f(std::integral_constant<int, ADAKV_F16>{});
+  else f(std::integral_constant<int, ADAKV_F32>{});
+}
+
+// Rows [G][D] of q (row g at element base + g * qsh) into LDS as fp32 times
+// `scale`; all loads of a thread are issued before the first is consumed.
+template <int NT, int GMAX, int D>
+__device__ __forceinline__ void stage_q(float (*s_q)[D], const void* q, int qdt, int64_t base, int64_t qsh,
+                                        int G, float scale) {
+  constexpr int IT = (GMAX * D + NT - 1) / NT;
+  with_dtype(qdt, [&](auto tag) {
+    constexpr int DT = decltype(tag)::value;
+    float x[IT];
+#pragma unroll
+    for (int u = 0; u < IT; ++u) {
+      const int i = min((int)threadIdx.x + u * NT, G * D - 1);     // in-bounds for every lane
+      x[u] = load_t<DT>(q, base + (int64_t)(i / D) * qsh + i % D);
+    }
+#pragma unroll
+    for (int u = 0; u < IT; ++u) {
+      const int i = threadIdx.x + u * NT;
+      if (i < G * D) s_q[i / D][i % D] = x[u] * scale;
+    }
+  });
 }
 
 // Scalar load of element i of a typed array (used for q and small tails).

@@ -1,5 +1,5 @@
 // Ragged block-sparse split-K flash-decode (adakv/kernels/block_sparse_decode.py:51-100)
-// and the dense split-K flash-decode baseline, one kernel for both.
+// and the dense split-K flash-decode baseline.
 //
 // Grid (split, KV head, sequence).  A workgroup serves the G q-heads of one KV
 // head.  Sparse mode first fixes each head's block count -- read from sel_lens,
@@ -12,15 +12,26 @@
 // `min_per` blocks, so the common small selection is served by one workgroup
 // and needs no merge.
 //
-// Inside a workgroup every wave streams its blocks with double-buffered 16-byte
-// loads: a lane owns one 16-byte slice of head_dim for one token row, so a
-// 16-token bf16 block of K (or V) is four coalesced loads per lane.  Scores of
-// every q-head that selected the block come from one read of K; each group of
-// lanes sharing a token row keeps its own online softmax (running max,
-// denominator, fp32 accumulator, exp2 domain), so no cross-row exchange happens
-// per block.  Row groups and waves are combined once at the end.  Several
-// active slices write (m, l, acc[D]) partials; in sparse mode the last slice
-// to arrive merges them, in dense mode merge_kernel does.
+// Streaming, bf16 / fp16 K and V (matrix cores): each wave takes 16-token
+// tiles.  S^T = K . Q^T runs on v_mfma_f32_16x16x32 -- K is loaded straight
+// into the A-operand layout (lane l holds token l%16 and a contiguous D/2-byte
+// slice of its row, so a tile is D/32 coalesced 16-byte loads per lane) and
+// the group's q-heads, zero-padded to 16, form the B operand.  The online
+// softmax runs on the 16x16 result (4 tokens per lane, the cross-lane max over
+// the 4 lane groups by permlane swaps), and O += P . V runs on
+// v_mfma_f32_16x16x16 with P taken directly from the S^T result layout and V
+// transposed through a per-wave LDS tile.  A 16-token tile costs 3*D/32
+// matrix instructions and a few dozen VALU instructions.
+//
+// Streaming, fp32 K and V (exact-parity mode): VALU dot products, a lane owns
+// a 16-byte slice of head_dim of one token row, each group of lanes sharing a
+// token row keeps its own online softmax and the row groups are combined once
+// at the end.
+//
+// Several active slices write (m, l, acc[D]) partials; in sparse mode the last
+// slice to arrive merges them, in dense mode merge_kernel does.
+#include <algorithm>
+
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -28,67 +39,53 @@ namespace adakv {
 namespace {
 
 constexpr int kSparseThreads = 512;
+constexpr int kDenseThreads = 256;
 
-template <int KVDT, int D, int GMAX, int NT>
-__global__ __launch_bounds__(NT) void decode_kernel(DecodeArgs a) {
-  constexpr int NW = NT / kWave;
-  constexpr int EPV = Elt<KVDT>::kPerVec;
-  constexpr int EB = Elt<KVDT>::kBytes;
-  constexpr int LPR = D / EPV;                 // lanes per token row
-  constexpr int RPL = kWave / LPR;             // token rows per wave-wide load
-  constexpr int NLD0 = 16 / RPL;
-  constexpr int NLD = NLD0 < 1 ? 1 : (NLD0 > 4 ? 4 : NLD0);   // <= 64 VGPRs of K/V tiles
-  constexpr int TT = RPL * NLD;                // tokens per sub-tile
-  extern __shared__ __align__(16) unsigned char s_dyn_raw[];
-  __shared__ float s_q[GMAX][D];
-  constexpr int HC0 = 8192 / (NW * D);          // heads merged per pass: <= 32 KiB of LDS
-  constexpr int HC = HC0 < 1 ? 1 : (HC0 > GMAX ? GMAX : HC0);
-  __shared__ float s_acc[NW][HC][D];
-  __shared__ float s_m[NW][GMAX], s_l[NW][GMAX];
-  __shared__ int s_cnt[GMAX];
-  __shared__ double s_wsum;
-  __shared__ int s_misc[NW + 2];
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
-  const int seg = lane % LPR, rsub = lane / LPR;
-  const int G = a.G;
-  const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
-  const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
-  const bool dense = a.table == nullptr;
+// ---------------------------------------------------------------------------
+// Prologue: per-head counts and the union list of one (sequence, KV head), and
+// this workgroup's slice [lo, hi) of it.
+// ---------------------------------------------------------------------------
+struct Slice {
+  int U, lo, hi, n_active;
+};
+
+__device__ __forceinline__ uint32_t* list_base(const DecodeArgs& a, unsigned char* s_dyn_raw) {
+  return reinterpret_cast<uint32_t*>(s_dyn_raw + ((a.Hq * 8 + 15) / 16) * 16) + ceil_div(a.max_blocks, 4);
+}
+
+template <int NT>
+__device__ Slice build_slice(const DecodeArgs& a, int b, int kvh, int split, int nb,
+                             unsigned char* s_dyn_raw, int* s_cnt, int* s_misc) {
+  const int tid = threadIdx.x, G = a.G;
   double* s_w = reinterpret_cast<double*>(s_dyn_raw);
   uint32_t* s_bits = reinterpret_cast<uint32_t*>(s_dyn_raw + ((a.Hq * 8 + 15) / 16) * 16);
-  uint32_t* s_list = s_bits + ceil_div(a.max_blocks, 4);
-
-  for (int i = tid; i < G * D; i += NT)
-    s_q[i / D][i % D] = load_elt(a.q, a.qdt, (int64_t)b * a.qsb + (int64_t)(kvh * G + i / D) * a.qsh + i % D) *
-                        a.scale_log2;
-
-  // ---- per-head counts and the union of the group's blocks ----
-  // The table entries that can be selected are loaded up front (before the
-  // counts are known); the counts then decide which of them enter the union.
+  uint32_t* s_list = list_base(a, s_dyn_raw);
   int U = nb, off = 0, w0 = 0, w1 = 0;
-  if (!dense) {
+  if (a.table != nullptr) {
+    // The table entries that can be selected are loaded up front (before the
+    // counts are known); the counts then decide which of them enter the union.
     const Bounds bb = budget_bounds(nb, a.cfg);
     const bool derive = a.sel_lens == nullptr;
     const bool adaptive = derive && a.cfg.policy == ADAKV_POLICY_ADAPTIVE && nb > 1;
     const int width = derive ? min(a.T, max(bb.kcap, 0)) : a.T;
     const int nwords = ceil_div(nb, 4);
-    for (int i = tid; i < nwords; i += NT) s_bits[i] = 0;
-    if (adaptive)
-      for (int h = tid; h < a.Hq; h += NT) s_w[h] = a.wbuf[(int64_t)b * a.Hq + h];
-    if (!derive && tid < G) s_cnt[tid] = min(max(a.sel_lens[(int64_t)b * a.Hq + kvh * G + tid], 0), a.T);
     constexpr int EPT = 4;                       // table entries per thread
     int ent[EPT];
 #pragma unroll
     for (int u = 0; u < EPT; ++u) {
-      const int e = tid + u * NT;
-      ent[u] = -1;
-      if (e < G * width) {
-        const int g = e / width, j = e % width;
-        ent[u] = a.table[((int64_t)b * a.Hq + kvh * G + g) * a.T + j];
-      }
+      const int e = min(tid + u * NT, max(G * width - 1, 0));   // in bounds; extra entries unused
+      ent[u] = a.table[((int64_t)b * a.Hq + kvh * G + e / width) * a.T + e % width];
     }
+    for (int i = tid; i < nwords; i += NT) s_bits[i] = 0;
+    if (adaptive)
+      for (int h = tid; h < a.Hq; h += NT) s_w[h] = a.wbuf[(int64_t)b * a.Hq + h];
+    if (!derive && tid < G) s_cnt[tid] = min(max(a.sel_lens[(int64_t)b * a.Hq + kvh * G + tid], 0), a.T);
     __syncthreads();
     if (derive) {
       // every thread evaluates the same sum of weights in NumPy's order
@@ -124,18 +121,13 @@ __global__ __launch_bounds__(NT) void decode_kernel(DecodeArgs a) {
     }
     off = block_excl_scan<NT>(cnt, s_misc, &U);
   }
+  Slice r;
+  r.U = U;
   const int per = U > 0 ? max(ceil_div(U, a.nsplit), a.min_per) : 0;
-  const int n_active = U > 0 ? ceil_div(U, per) : 0;
-  const int lo_e = split * per, hi_e = min(U, lo_e + per);
-  if (U == 0) {
-    // no valid block for any head of the group: 0/0, as the reference kernel
-    if (split == 0)
-      for (int i = tid; i < G * D; i += NT)
-        store_elt(a.out, a.odt, (int64_t)b * a.osb + (int64_t)(kvh * G + i / D) * a.osh + i % D, __builtin_nanf(""));
-    return;
-  }
-  if (lo_e >= hi_e) return;
-  if (!dense) {
+  r.n_active = U > 0 ? ceil_div(U, per) : 0;
+  r.lo = split * per;
+  r.hi = min(U, r.lo + per);
+  if (a.table != nullptr && r.lo < r.hi) {
     int p = off;
     for (int i = w0; i < w1; ++i) {
       const uint32_t x = s_bits[i];
@@ -143,15 +135,188 @@ __global__ __launch_bounds__(NT) void decode_kernel(DecodeArgs a) {
       for (int j = 0; j < 4; ++j) {
         const uint32_t m8 = (x >> (8 * j)) & 0xffu;
         if (m8) {
-          if (p >= lo_e && p < hi_e) s_list[p - lo_e] = (uint32_t)(4 * i + j) | (m8 << 24);
+          if (p >= r.lo && p < r.hi) s_list[p - r.lo] = (uint32_t)(4 * i + j) | (m8 << 24);
           ++p;
         }
       }
     }
   }
   __syncthreads();
+  return r;
+}
 
-  // ---- stream this split's blocks ----
+// Block id and head mask of entry e (slice-relative) of the list.
+__device__ __forceinline__ void list_entry(const DecodeArgs& a, const uint32_t* s_list, int lo, int e,
+                                           int& blk, uint32_t& hm) {
+  if (a.table == nullptr) {
+    blk = lo + e;
+    hm = (1u << a.G) - 1u;
+  } else {
+    const uint32_t ent = s_list[e];
+    blk = (int)(ent & 0xffffffu);
+    hm = ent >> 24;
+  }
+}
+
+__device__ __forceinline__ void write_nan_outputs(const DecodeArgs& a, int b, int kvh, int D, int NT) {
+  // no valid block for any head of the group: 0/0, as the reference kernel
+  for (int i = threadIdx.x; i < a.G * D; i += NT)
+    store_elt(a.out, a.odt, (int64_t)b * a.osb + (int64_t)(kvh * a.G + i / D) * a.osh + i % D,
+              __builtin_nanf(""));
+}
+
+// ---------------------------------------------------------------------------
+// Epilogue: combine the waves' (m, l, acc) through LDS -- s_m, s_l [NW][GMAX],
+// s_acc [NW][HC][D] reused for head chunks of HC; stage(g0, n) writes the acc
+// of heads g0 .. g0+n-1 of the calling wave -- then write the output (single
+// active slice) or this slice's partials; in sparse mode the last slice to
+// arrive merges all partials.
+// ---------------------------------------------------------------------------
+template <int NT, int D, int GMAX, int HC, typename Stage>
+__device__ void finish(const DecodeArgs& a, int b, int kvh, int split, const Slice& sl,
+                       float (*s_m)[GMAX], float (*s_l)[GMAX], float (*s_acc)[HC][D], int* s_misc,
+                       Stage stage) {
+  constexpr int NW = NT / kWave;
+  const int tid = threadIdx.x, G = a.G;
+  float* part = a.partials + (((int64_t)b * a.Hkv + kvh) * a.nsplit) * G * (D + 2);
+  const int64_t pstride = (int64_t)G * (D + 2);
+#pragma unroll
+  for (int g0 = 0; g0 < GMAX; g0 += HC) {
+    if (g0 >= G) break;                      // uniform over the workgroup
+    const int n = min(HC, G - g0);
+    stage(g0, n);
+    __syncthreads();
+    for (int i = tid; i < n * D; i += NT) {
+      const int gg = i / D, g = g0 + gg, d = i % D;
+      float M = s_m[0][g];
+#pragma unroll
+      for (int ww = 1; ww < NW; ++ww) M = fmaxf(M, s_m[ww][g]);
+      float L = 0.f, O = 0.f;
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) {
+          const float f = s_m[ww][g] == -INFINITY ? 0.f : exp2f(s_m[ww][g] - M);
+          L += s_l[ww][g] * f;
+          O += s_acc[ww][gg][d] * f;
+        }
+      }
+      if (sl.n_active == 1) {
+        store_elt(a.out, a.odt, (int64_t)b * a.osb + (int64_t)(kvh * G + g) * a.osh + d, O / L);
+      } else {
+        float* pg = part + split * pstride + g * (D + 2);
+        pg[2 + d] = O;
+        if (d == 0) { pg[0] = M; pg[1] = L; }
+      }
+    }
+    __syncthreads();
+  }
+  if (sl.n_active == 1 || !a.merge_in_kernel) return;
+
+  // sparse: the last active slice merges (at most nsplit <= 16 of them)
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) s_misc[NW] = arrive(&a.counters[(int64_t)b * a.Hkv + kvh]) == sl.n_active - 1;
+  __syncthreads();
+  if (!s_misc[NW]) return;
+  __threadfence();
+  for (int i = tid; i < G * D; i += NT) {
+    const int g = i / D, d = i % D;
+    const float* pg = part + g * (D + 2);
+    float ms[16], ls[16], os[16];
+#pragma unroll
+    for (int sp = 0; sp < 16; ++sp) {
+      const bool ok = sp < sl.n_active;
+      ms[sp] = ok ? pg[sp * pstride] : -INFINITY;
+      ls[sp] = ok ? pg[sp * pstride + 1] : 0.f;
+      os[sp] = ok ? pg[sp * pstride + 2 + d] : 0.f;
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int sp = 0; sp < 16; ++sp) M = fmaxf(M, ms[sp]);
+    float L = 0.f, O = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int sp = 0; sp < 16; ++sp) {
+        const float f = ms[sp] == -INFINITY ? 0.f : exp2f(ms[sp] - M);
+        L += ls[sp] * f;
+        O += os[sp] * f;
+      }
+    }
+    store_elt(a.out, a.odt, (int64_t)b * a.osb + (int64_t)(kvh * G + g) * a.osh + d, O / L);
+  }
+  if (tid == 0) reset_counter(&a.counters[(int64_t)b * a.Hkv + kvh]);
+}
+
+// Streams items j = w, w + NW, ... of a slice with one item in flight while
+// the previous one is computed.  item(j, t_lo, t_hi, hm) describes item j,
+// load(t_lo, t_hi, bufs...) issues its loads, compute(t_lo, t_hi, hm, bufs...)
+// consumes them.
+template <int NW, typename Buf, typename Item, typename Load, typename Compute>
+__device__ __forceinline__ void stream_items(int w, int n_items, Item item, Load load, Compute compute) {
+  Buf A, B;
+  int alo = 0, ahi = 0, blo = 0, bhi = 0;
+  uint32_t ahm = 0, bhm = 0;
+  int j = w;
+  if (j < n_items) {
+    item(j, alo, ahi, ahm);
+    load(alo, ahi, A);
+  }
+  while (j < n_items) {
+    const int j2 = j + NW;
+    if (j2 < n_items) {
+      item(j2, blo, bhi, bhm);
+      load(blo, bhi, B);
+    }
+    compute(alo, ahi, ahm, A);
+    if (j2 >= n_items) break;
+    const int j3 = j2 + NW;
+    if (j3 < n_items) {
+      item(j3, alo, ahi, ahm);
+      load(alo, ahi, A);
+    }
+    compute(blo, bhi, bhm, B);
+    j = j3;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// VALU streaming kernel (fp32 K/V).
+// ---------------------------------------------------------------------------
+template <int KVDT, int D, int GMAX, int NT>
+__global__ __launch_bounds__(NT) void decode_kernel(DecodeArgs a) {
+  constexpr int NW = NT / kWave;
+  constexpr int EPV = Elt<KVDT>::kPerVec;
+  constexpr int EB = Elt<KVDT>::kBytes;
+  constexpr int LPR = D / EPV;                 // lanes per token row
+  constexpr int RPL = kWave / LPR;             // token rows per wave-wide load
+  constexpr int NLD0 = 16 / RPL;
+  constexpr int NLD = NLD0 < 1 ? 1 : (NLD0 > 4 ? 4 : NLD0);   // <= 64 VGPRs of K/V tiles
+  constexpr int TT = RPL * NLD;                // tokens per sub-tile
+  constexpr int HC0 = 8192 / (NW * D);         // heads merged per pass: <= 32 KiB of LDS
+  constexpr int HC = HC0 < 1 ? 1 : (HC0 > GMAX ? GMAX : HC0);
+  extern __shared__ __align__(16) unsigned char s_dyn_raw[];
+  __shared__ float s_q[GMAX][D];
+  __shared__ float s_acc[NW][HC][D];
+  __shared__ float s_m[NW][GMAX], s_l[NW][GMAX];
+  __shared__ int s_cnt[GMAX];
+  __shared__ int s_misc[NW + 2];
+
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  const int seg = lane % LPR, rsub = lane / LPR;
+  const int G = a.G;
+  const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
+  const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
+
+  stage_q<NT, GMAX, D>(s_q, a.q, a.qdt, (int64_t)b * a.qsb + (int64_t)kvh * G * a.qsh, a.qsh, G, a.scale_log2);
+  const Slice sl = build_slice<NT>(a, b, kvh, split, nb, s_dyn_raw, s_cnt, s_misc);
+  if (sl.U == 0) {
+    if (split == 0) write_nan_outputs(a, b, kvh, D, NT);
+    return;
+  }
+  if (sl.lo >= sl.hi) return;
+  const uint32_t* s_list = list_base(a, s_dyn_raw);
+
   // q lives in registers, except for groups of 8 heads where it is read from
   // LDS at each use to leave the registers to the double-buffered K/V tiles.
   constexpr bool kQRegs = GMAX < 8;
@@ -178,41 +343,34 @@ __global__ __launch_bounds__(NT) void decode_kernel(DecodeArgs a) {
   const char* kbase = reinterpret_cast<const char*>(a.k) + head_off;
   const char* vbase = reinterpret_cast<const char*>(a.v) + head_off;
   const int64_t row_bytes = a.ss * EB;
-  const uint32_t all_heads = (1u << G) - 1u;
   const int n_sub = ceil_div(a.bs, TT);
-  const int n_items = (hi_e - lo_e) * n_sub;
+  const int n_items = (sl.hi - sl.lo) * n_sub;
 
+  struct Buf { uint4 k[NLD], v[NLD]; };
   // item j: sub-tile (j % n_sub) of list entry (j / n_sub)
   auto item = [&](int j, int& t_lo, int& t_hi, uint32_t& hm) {
-    const int e = lo_e + j / n_sub;
     int blk;
-    if (dense) {
-      blk = e;
-      hm = all_heads;
-    } else {
-      const uint32_t ent = s_list[e - lo_e];
-      blk = (int)(ent & 0xffffffu);
-      hm = ent >> 24;
-    }
+    list_entry(a, s_list, sl.lo, j / n_sub, blk, hm);
     t_lo = blk * a.bs + (j % n_sub) * TT;
     t_hi = min(min(blk * a.bs + a.bs, len), t_lo + TT);
   };
-  auto load = [&](int t_lo, int t_hi, uint4* kr, uint4* vr) {
+  // Rows past the tile's end load the tile's last row instead (always in
+  // bounds, so the loads need no predication); their scores are masked.
+  auto load = [&](int t_lo, int t_hi, Buf& r) {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
-      const int t = t_lo + i * RPL + rsub;
-      const int64_t o = (int64_t)t * row_bytes;
-      kr[i] = t < t_hi ? load16(kbase + o) : make_uint4(0, 0, 0, 0);
-      vr[i] = t < t_hi ? load16(vbase + o) : make_uint4(0, 0, 0, 0);
+      const int64_t o = (int64_t)min(t_lo + i * RPL + rsub, t_hi - 1) * row_bytes;
+      r.k[i] = load16(kbase + o);
+      r.v[i] = load16(vbase + o);
     }
   };
-  auto compute = [&](int t_lo, int t_hi, uint32_t hm, const uint4* kr, const uint4* vr) {
+  auto compute = [&](int t_lo, int t_hi, uint32_t hm, const Buf& r) {
     // scores of every active head for this lane's NLD token rows
     float s[GMAX][NLD];
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       float kx[EPV];
-      unpack<KVDT>(kr[i], kx);
+      unpack<KVDT>(r.k[i], kx);
       const bool valid = t_lo + i * RPL + rsub < t_hi;
 #pragma unroll
       for (int g = 0; g < GMAX; ++g) {
@@ -254,7 +412,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       float vx[EPV];
-      unpack<KVDT>(vr[i], vx);
+      unpack<KVDT>(r.v[i], vx);
 #pragma unroll
       for (int g = 0; g < GMAX; ++g) {
         if (g < G && ((hm >> g) & 1u)) {
@@ -264,35 +422,9 @@ __global__ __launch_bounds__(NT) void decode_kernel(DecodeArgs a) {
       }
     }
   };
+  stream_items<NW, Buf>(w, n_items, item, load, compute);
 
-  {
-    uint4 ka[NLD], va[NLD], kb[NLD], vb[NLD];
-    int alo = 0, ahi = 0, blo = 0, bhi = 0;
-    uint32_t ahm = 0, bhm = 0;
-    int j = w;
-    if (j < n_items) {
-      item(j, alo, ahi, ahm);
-      load(alo, ahi, ka, va);
-    }
-    while (j < n_items) {
-      const int j2 = j + NW;
-      if (j2 < n_items) {
-        item(j2, blo, bhi, bhm);
-        load(blo, bhi, kb, vb);
-      }
-      compute(alo, ahi, ahm, ka, va);
-      if (j2 >= n_items) break;
-      const int j3 = j2 + NW;
-      if (j3 < n_items) {
-        item(j3, alo, ahi, ahm);
-        load(alo, ahi, ka, va);
-      }
-      compute(blo, bhi, bhm, kb, vb);
-      j = j3;
-    }
-  }
-
-  // ---- combine the row groups of the wave (lanes with the same slice) ----
+  // combine the row groups of the wave (lanes with the same slice)
   auto merge_pair = [&](int g, float ma, float mb, float la, float lb, const float* aa, const float* ab) {
     const float mn = fmaxf(ma, mb);
     const float fa = ma == -INFINITY ? 0.f : exp2f(ma - mn);
@@ -338,80 +470,216 @@ __global__ __launch_bounds__(NT) void decode_kernel(DecodeArgs a) {
       }
     }
   }
-
-  // ---- combine the waves, HC heads per LDS pass ----
-  float* part = a.partials + (((int64_t)b * a.Hkv + kvh) * a.nsplit) * G * (D + 2);
-  const int64_t pstride = (int64_t)G * (D + 2);
-#pragma unroll
-  for (int g0 = 0; g0 < GMAX; g0 += HC) {
-    if (g0 >= G) break;                      // uniform over the workgroup
+  finish<NT, D, GMAX, HC>(a, b, kvh, split, sl, s_m, s_l, s_acc, s_misc, [&](int g0, int n) {
     if (rsub == 0) {
 #pragma unroll
       for (int gg = 0; gg < HC; ++gg)
-        if (g0 + gg < G)
+        if (gg < n)
 #pragma unroll
           for (int e = 0; e < EPV; ++e) s_acc[w][gg][seg * EPV + e] = acc[g0 + gg][e];
     }
-    __syncthreads();
-    for (int i = tid; i < min(HC, G - g0) * D; i += NT) {
-      const int gg = i / D, g = g0 + gg, d = i % D;
-      float M = s_m[0][g];
-#pragma unroll
-      for (int ww = 1; ww < NW; ++ww) M = fmaxf(M, s_m[ww][g]);
-      float L = 0.f, O = 0.f;
-      if (M != -INFINITY) {
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww) {
-          const float f = s_m[ww][g] == -INFINITY ? 0.f : exp2f(s_m[ww][g] - M);
-          L += s_l[ww][g] * f;
-          O += s_acc[ww][gg][d] * f;
-        }
-      }
-      if (n_active == 1) {
-        store_elt(a.out, a.odt, (int64_t)b * a.osb + (int64_t)(kvh * G + g) * a.osh + d, O / L);
-      } else {
-        float* pg = part + split * pstride + g * (D + 2);
-        pg[2 + d] = O;
-        if (d == 0) { pg[0] = M; pg[1] = L; }
-      }
-    }
-    __syncthreads();
-  }
-  if (n_active == 1 || !a.merge_in_kernel) return;
+  });
+}
 
-  // ---- sparse: the last active split merges (at most nsplit <= 16 of them) ----
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_misc[NW] = arrive(&a.counters[(int64_t)b * a.Hkv + kvh]) == n_active - 1;
-  __syncthreads();
-  if (!s_misc[NW]) return;
-  __threadfence();
-  for (int i = tid; i < G * D; i += NT) {
-    const int g = i / D, d = i % D;
-    const float* pg = part + g * (D + 2);
-    float ms[16], ls[16], os[16];
+// ---------------------------------------------------------------------------
+// Matrix-core streaming kernel (bf16 / fp16 K/V).
+// ---------------------------------------------------------------------------
+template <int KVDT>
+__device__ __forceinline__ float4_t mfma_qk(const uint4& k, const uint4& q, float4_t c) {
+  if constexpr (KVDT == ADAKV_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, k),
+                                                   __builtin_bit_cast(bf16x8_t, q), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, k),
+                                                  __builtin_bit_cast(f16x8_t, q), c, 0, 0, 0);
+}
+template <int KVDT>
+__device__ __forceinline__ float4_t mfma_pv(const uint2& p, const uint2& v, float4_t c) {
+  if constexpr (KVDT == ADAKV_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_t, p),
+                                                     __builtin_bit_cast(short4_t, v), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, p),
+                                                 __builtin_bit_cast(f16x4_t, v), c, 0, 0, 0);
+}
+template <int KVDT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  if constexpr (KVDT == ADAKV_BF16) return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  else return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+}
+
+template <int D, int NT, int GMAX>
+struct MfmaShape {
+  static constexpr int NW = NT / kWave;
+  static constexpr int KS = D / 32;            // k-steps of S^T = K . Q^T (16-byte loads per lane)
+  static constexpr int NT16 = D / 16;          // 16-column tiles of O
+  static constexpr int VROW = D / 2 + 2;       // V tile row stride in 4-byte words (conflict-free reads)
+  static constexpr int VT_WORDS = 16 * VROW;
+  static constexpr int HC0 = 8192 / (NW * D);
+  static constexpr int HC = HC0 < 1 ? 1 : (HC0 > GMAX ? GMAX : HC0);   // heads merged per LDS pass
+  static constexpr int BIG_WORDS = (NW * VT_WORDS > NW * HC * D) ? NW * VT_WORDS : NW * HC * D;
+};
+
+template <int KVDT, int D, int GMAX, int NT>
+__global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeArgs a) {
+  static_assert(D % 32 == 0 && GMAX <= 16, "16x16 tiles over head_dim, at most 16 q-heads per group");
+  using S = MfmaShape<D, NT, GMAX>;
+  constexpr int NW = S::NW, KS = S::KS, NT16 = S::NT16, VROW = S::VROW, HC = S::HC;
+  extern __shared__ __align__(16) unsigned char s_dyn_raw[];
+  __shared__ __align__(16) uint32_t s_big[S::BIG_WORDS];    // V tiles while streaming, then the merge
+  __shared__ float s_m[NW][GMAX], s_l[NW][GMAX];
+  __shared__ int s_cnt[GMAX];
+  __shared__ int s_misc[NW + 2];
+
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  const int col = lane & 15, grp = lane >> 4;     // MFMA lane coordinates
+  const int G = a.G;
+  const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
+  const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
+
+  // B operand of S^T: lane (col, grp) holds q[head col][D/4*grp + 8*s .. +7] at step s
+  // (the same permutation of head_dim as the K fragments, so the dot products are whole)
+  uint4 qf[KS];
+  with_dtype(a.qdt, [&](auto tag) {
+    constexpr int QDT = decltype(tag)::value;
+    const int64_t qo = (int64_t)b * a.qsb + (int64_t)(kvh * G + min(col, G - 1)) * a.qsh + (D / 4) * grp;
+    float x[KS][8];
 #pragma unroll
-    for (int sp = 0; sp < 16; ++sp) {
-      const bool ok = sp < n_active;
-      ms[sp] = ok ? pg[sp * pstride] : -INFINITY;
-      ls[sp] = ok ? pg[sp * pstride + 1] : 0.f;
-      os[sp] = ok ? pg[sp * pstride + 2 + d] : 0.f;
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) x[s][t] = load_t<QDT>(a.q, qo + 8 * s + t);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      uint32_t wv[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) wv[t] = col < G ? pack2<KVDT>(x[s][2 * t], x[s][2 * t + 1]) : 0u;
+      qf[s] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
     }
-    float M = -INFINITY;
-#pragma unroll
-    for (int sp = 0; sp < 16; ++sp) M = fmaxf(M, ms[sp]);
-    float L = 0.f, O = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int sp = 0; sp < 16; ++sp) {
-        const float f = ms[sp] == -INFINITY ? 0.f : exp2f(ms[sp] - M);
-        L += ls[sp] * f;
-        O += os[sp] * f;
-      }
-    }
-    store_elt(a.out, a.odt, (int64_t)b * a.osb + (int64_t)(kvh * G + g) * a.osh + d, O / L);
+  });
+  const Slice sl = build_slice<NT>(a, b, kvh, split, nb, s_dyn_raw, s_cnt, s_misc);
+  if (sl.U == 0) {
+    if (split == 0) write_nan_outputs(a, b, kvh, D, NT);
+    return;
   }
-  if (tid == 0) reset_counter(&a.counters[(int64_t)b * a.Hkv + kvh]);
+  if (sl.lo >= sl.hi) return;
+  const uint32_t* s_list = list_base(a, s_dyn_raw);
+
+  // lane (col, grp) loads token col of a 16-token tile, elements [D/4*grp, D/4*(grp+1)) of its row
+  const int64_t head_off = ((int64_t)b * a.sb + (int64_t)kvh * a.sh + (D / 4) * grp) * 2;
+  const char* kbase = reinterpret_cast<const char*>(a.k) + head_off;
+  const char* vbase = reinterpret_cast<const char*>(a.v) + head_off;
+  const int64_t row_bytes = a.ss * 2;
+  const int n_sub = ceil_div(a.bs, 16);
+  const int n_items = (sl.hi - sl.lo) * n_sub;
+  uint32_t* vt = s_big + w * S::VT_WORDS;         // this wave's V tile [16 tokens][VROW words]
+  const uint16_t* vt16 = reinterpret_cast<const uint16_t*>(vt);
+  const float scale = a.scale_log2;
+
+  float m_h = -INFINITY, l_h = 0.f;               // softmax state of head `col` (l: this lane's tokens)
+  float4_t acc[NT16];                             // O[head 4*grp+i][16*n + col]
+#pragma unroll
+  for (int n = 0; n < NT16; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  struct Buf { uint4 k[KS], v[KS]; };
+  auto item = [&](int j, int& t0, int& t_hi, uint32_t& hm) {
+    int blk;
+    list_entry(a, s_list, sl.lo, j / n_sub, blk, hm);
+    t0 = blk * a.bs + (j % n_sub) * 16;
+    t_hi = min(min(blk * a.bs + a.bs, len), t0 + 16);
+  };
+  // Tokens past the tile's end load the tile's last row instead (always in
+  // bounds, so the loads need no predication); their weights are zeroed.
+  auto load = [&](int t0, int t_hi, Buf& r) {
+    const int64_t o = (int64_t)min(t0 + col, t_hi - 1) * row_bytes;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      r.k[s] = load16(kbase + o + 16 * s);
+      r.v[s] = load16(vbase + o + 16 * s);
+    }
+  };
+  auto compute = [&](int t0, int t_hi, uint32_t hm, const Buf& r) {
+    // V rows to this wave's LDS tile for the transposed B-operand reads; the
+    // previous tile's reads were issued before these writes (LDS operations of
+    // a wave complete in order), the compiler barriers keep that order.
+    __asm__ volatile("" ::: "memory");
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      uint32_t* p = vt + col * VROW + (D / 8) * grp + 4 * s;
+      *reinterpret_cast<uint2*>(p) = make_uint2(r.v[s].x, r.v[s].y);
+      *reinterpret_cast<uint2*>(p + 2) = make_uint2(r.v[s].z, r.v[s].w);
+    }
+    __asm__ volatile("" ::: "memory");
+    // S^T[token 4*grp+i][head col]
+    float4_t sc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) sc = mfma_qk<KVDT>(r.k[s], qf[s], sc);
+    const bool head_on = col < G && ((hm >> col) & 1u);
+    float sv[4];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = head_on && (t0 + 4 * grp + i < t_hi);
+      sv[i] = ok ? sc[i] * scale : -INFINITY;
+      mt = fmaxf(mt, sv[i]);
+    }
+    LanePair pr = swap16(mt);
+    mt = fmaxf(pr.a, pr.b);
+    pr = swap32(mt);
+    mt = fmaxf(pr.a, pr.b);
+    const float mn = fmaxf(m_h, mt);
+    const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_h - mn);
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sv[i] = sv[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[i] - mn);
+      ps += sv[i];
+    }
+    l_h = l_h * alpha + ps;
+    m_h = mn;
+    // rescale the O rows (heads 4*grp+i) by their heads' alpha, held by lanes col == head
+    float al[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      al[i] = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * grp + i) * 4, __float_as_int(alpha)));
+#pragma unroll
+    for (int n = 0; n < NT16; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[n][i] *= al[i];
+    // O += P . V: A = P[head col][tokens 4*grp .. +3] (the S^T layout), B = V[tokens][16 dims]
+    const uint2 pf = make_uint2(pack2<KVDT>(sv[0], sv[1]), pack2<KVDT>(sv[2], sv[3]));
+#pragma unroll
+    for (int n = 0; n < NT16; ++n) {
+      const int c16 = n * 16 + col;
+      const uint32_t v0 = vt16[(4 * grp + 0) * 2 * VROW + c16], v1 = vt16[(4 * grp + 1) * 2 * VROW + c16];
+      const uint32_t v2 = vt16[(4 * grp + 2) * 2 * VROW + c16], v3 = vt16[(4 * grp + 3) * 2 * VROW + c16];
+      acc[n] = mfma_pv<KVDT>(pf, make_uint2(v0 | (v1 << 16), v2 | (v3 << 16)), acc[n]);
+    }
+  };
+  stream_items<NW, Buf>(w, n_items, item, load, compute);
+
+  // denominator of head col over the wave's 4 lane groups
+  {
+    LanePair pr = swap16(l_h);
+    l_h = pr.a + pr.b;
+    pr = swap32(l_h);
+    l_h = pr.a + pr.b;
+  }
+  if (grp == 0 && col < G) {
+    s_m[w][col] = m_h;
+    s_l[w][col] = l_h;
+  }
+  __syncthreads();                                  // the V tiles are dead: s_big becomes s_acc
+  auto s_acc = reinterpret_cast<float (*)[HC][D]>(s_big);
+  finish<NT, D, GMAX, HC>(a, b, kvh, split, sl, s_m, s_l, s_acc, s_misc, [&](int g0, int n) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int head = 4 * grp + i;
+      if (head >= g0 && head < g0 + n)
+#pragma unroll
+        for (int t = 0; t < NT16; ++t) s_acc[w][head - g0][t * 16 + col] = acc[t][i];
+    }
+  });
 }
 
 // Dense split-K merge: one workgroup per (q-head of the group, KV head, sequence).
@@ -460,23 +728,34 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   }
 }
 
-template <int KVDT, int D, int NT>
+template <int KVDT, int D, int NT, bool MFMA>
 hipError_t launch_g(const DecodeArgs& a, size_t dyn, hipStream_t s) {
   dim3 grid(a.nsplit, a.Hkv, a.B);
-  if (a.G <= 1) hipLaunchKernelGGL((decode_kernel<KVDT, D, 1, NT>), grid, dim3(NT), dyn, s, a);
-  else if (a.G <= 2) hipLaunchKernelGGL((decode_kernel<KVDT, D, 2, NT>), grid, dim3(NT), dyn, s, a);
-  else if (a.G <= 4) hipLaunchKernelGGL((decode_kernel<KVDT, D, 4, NT>), grid, dim3(NT), dyn, s, a);
-  else hipLaunchKernelGGL((decode_kernel<KVDT, D, 8, NT>), grid, dim3(NT), dyn, s, a);
+#define ADAKV_LAUNCH(GM)                                                                          \
+  do {                                                                                            \
+    if constexpr (MFMA)                                                                           \
+      hipLaunchKernelGGL((decode_mfma_kernel<KVDT, D, GM, NT>), grid, dim3(NT), dyn, s, a);       \
+    else                                                                                          \
+      hipLaunchKernelGGL((decode_kernel<KVDT, D, GM, NT>), grid, dim3(NT), dyn, s, a);            \
+  } while (0)
+  if (a.G <= 1) ADAKV_LAUNCH(1);
+  else if (a.G <= 2) ADAKV_LAUNCH(2);
+  else if (a.G <= 4) ADAKV_LAUNCH(4);
+  else ADAKV_LAUNCH(8);
+#undef ADAKV_LAUNCH
   return hipGetLastError();
 }
 
 template <int KVDT, int D>
 hipError_t launch_d(const DecodeArgs& a, hipStream_t s) {
+  constexpr bool kMfma = KVDT != ADAKV_F32;
   if (a.table) {
     const size_t dyn = ((size_t)a.Hq * 8 + 15) / 16 * 16 + (size_t)(((a.max_blocks + 3) / 4) + a.list_cap) * 4;
-    return launch_g<KVDT, D, kSparseThreads>(a, dyn, s);
+    // head_dim 256 in matrix-core mode: 4 waves keep the V tiles within 64 KiB
+    constexpr int NT = (kMfma && D >= 256) ? 256 : kSparseThreads;
+    return launch_g<KVDT, D, NT, kMfma>(a, dyn, s);
   }
-  return launch_g<KVDT, D, 256>(a, 16, s);
+  return launch_g<KVDT, D, kDenseThreads, kMfma>(a, 16, s);
 }
 
 template <int KVDT>
@@ -491,6 +770,23 @@ hipError_t launch_k(const DecodeArgs& a, int D, hipStream_t s) {
 }
 
 }  // namespace
+
+int decode_threads(int kvdt, int D, bool sparse) {
+  if (!sparse) return kDenseThreads;
+  return (kvdt != ADAKV_F32 && D >= 256) ? 256 : kSparseThreads;
+}
+
+size_t decode_static_lds(int kvdt, int D, int gmax, bool sparse) {
+  const int NW = decode_threads(kvdt, D, sparse) / kWave;
+  const size_t common = (size_t)2 * NW * gmax * 4 + (size_t)gmax * 4 + (size_t)(NW + 2) * 4;
+  if (kvdt == ADAKV_F32) {
+    const int hc = std::max(1, std::min(gmax, 8192 / (NW * D)));
+    return common + (size_t)gmax * D * 4 + (size_t)NW * hc * D * 4;
+  }
+  const int hc = std::max(1, std::min(gmax, 8192 / (NW * D)));
+  const size_t vt = (size_t)NW * 16 * (D / 2 + 2) * 4, mrg = (size_t)NW * hc * D * 4;
+  return common + std::max(vt, mrg);
+}
 
 hipError_t launch_decode(const DecodeArgs& a, int kvdt, int D, hipStream_t s) {
   switch (kvdt) {

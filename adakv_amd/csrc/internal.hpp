@@ -37,6 +37,7 @@ struct ScoreArgs {
   const void* k;
   int kdt;
   int64_t ksb, ksh, kss;
+  int n_app, n_chunks;         // set by the launcher: workgroups per (sequence, KV head)
 };
 
 struct SelectArgs {
@@ -113,6 +114,10 @@ hipError_t launch_score(const ScoreArgs& a, int cdt, int D, hipStream_t s);
 hipError_t launch_select(const SelectArgs& a, int max_blocks, hipStream_t s);
 hipError_t launch_budget(const BudgetArgs& a, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs& a, int kvdt, int D, hipStream_t s);
+// Threads per workgroup and static LDS bytes of the decode kernel chosen for
+// (K/V dtype, head_dim, group size rounded up to a power of two, mode).
+int decode_threads(int kvdt, int D, bool sparse);
+size_t decode_static_lds(int kvdt, int D, int gmax, bool sparse);
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 
 }  // namespace adakv

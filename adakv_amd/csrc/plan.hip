@@ -3,13 +3,12 @@
 // NumPy oracle: adakv/estimator.py:62-74, adakv/budget.py:28-86,
 // adakv/selector.py:18-60).
 //
-// score_kernel   one workgroup per (sequence, KV head, chunk of 64 blocks).  The
-//                G query heads of the group are staged once through LDS into
-//                registers; every centroid row is read once with 16-byte loads
-//                and dotted with all G queries (fp32 FMA, then a DPP butterfly
-//                over the lanes sharing the row).  The workgroup owning the
-//                newest block(s) first recomputes their centroids from K
-//                (the decode-time append), so no separate launch is needed.
+// score_kernel   one workgroup per (sequence, KV head, chunk of CB blocks)
+//                dotting every centroid row with the G query heads of the
+//                group, plus one workgroup per appended block (the
+//                decode-time centroid append), dispatched first, which
+//                recomputes that block's centroid from K and scores it -- no
+//                separate append launch.
 // select_kernel  one workgroup per (sequence, q-head).  Holds the head's scores
 //                in registers, computes the normalised softmax entropy, picks
 //                the top content blocks with a linear-bin radix select plus a
@@ -22,6 +21,8 @@
 //                counts itself).
 #include <float.h>
 
+#include <algorithm>
+
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -31,26 +32,6 @@ namespace {
 constexpr int kNT = 256;
 constexpr int kSortCap = 512;
 
-// N consecutive key elements of runtime type kdt starting at p (8- or 16-byte
-// aligned), widened to fp32.
-template <int N>
-__device__ __forceinline__ void load_slice(const char* p, int kdt, float* out) {
-  if (kdt == ADAKV_F32) {
-#pragma unroll
-    for (int i = 0; i < N / 4; ++i) unpack<ADAKV_F32>(load16(p + 16 * i), out + 4 * i);
-  } else if constexpr (N == 8) {
-    const uint4 v = load16(p);
-    if (kdt == ADAKV_BF16) unpack<ADAKV_BF16>(v, out); else unpack<ADAKV_F16>(v, out);
-  } else {
-    const uint2 v = *reinterpret_cast<const uint2*>(p);
-    const uint4 w = make_uint4(v.x, v.y, 0, 0);
-    float t[8];
-    if (kdt == ADAKV_BF16) unpack<ADAKV_BF16>(w, t); else unpack<ADAKV_F16>(w, t);
-#pragma unroll
-    for (int i = 0; i < N; ++i) out[i] = t[i];
-  }
-}
-
 __device__ __forceinline__ float round_to(float x, int dt) {
   if (dt == ADAKV_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(x));
   if (dt == ADAKV_F16) return f16_bits_to_f32(f32_to_f16_bits(x));
@@ -58,6 +39,69 @@ __device__ __forceinline__ float round_to(float x, int dt) {
 }
 
 // ---------------------------------------------------------------- scores ----
+// Decode-time append (adakv/estimator.py:62-74): block r gained tokens, so its
+// centroid becomes the sequential fp32 mean of its real tokens (summed in
+// token order, one correctly rounded division, one rounding to the centroid
+// type); the new centroid is stored and scored against the G q-heads.  One
+// workgroup per appended block: each pass loads up to kNT / (D / 8) token rows
+// at once with 16-byte loads, stages them through LDS and adds them column by
+// column in token order.
+template <int CDT, int KDT, int D, int GMAX>
+__device__ void append_block(const ScoreArgs& a, int b, int kvh, int r, int len, const float (*s_q)[D],
+                             float* s_tile, float (*s_red)[kNT / kWave]) {
+  constexpr int EPV = Elt<KDT>::kPerVec;
+  constexpr int EB = Elt<KDT>::kBytes;
+  constexpr int LPR = D / EPV;                 // lanes per token row
+  constexpr int RP = kNT / LPR;                // token rows per pass
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  const int row = tid / LPR, seg = tid % LPR;
+  const int t0 = r * a.bs, t1 = min(t0 + a.bs, len);
+  const char* kp = reinterpret_cast<const char*>(a.k) +
+                   ((int64_t)b * a.ksb + (int64_t)kvh * a.ksh + seg * EPV) * EB;
+  float acc = 0.f;
+  for (int p0 = t0; p0 < t1; p0 += RP) {
+    const int t = min(p0 + row, t1 - 1);       // in bounds; rows past t1 are not summed
+    float x[EPV];
+    unpack<KDT>(load16(kp + (int64_t)t * a.kss * EB), x);
+    __syncthreads();                           // the previous pass's tile has been consumed
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) s_tile[row * D + seg * EPV + e] = x[e];
+    __syncthreads();
+    if (tid < D) {
+      const int n = min(RP, t1 - p0);
+      for (int j = 0; j < n; ++j) acc = (p0 + j == t0) ? s_tile[j * D + tid] : acc + s_tile[j * D + tid];
+    }
+  }
+  float c = 0.f;
+  if (tid < D) {
+    const float m = __fdiv_rn(acc, (float)(t1 - t0));
+    store_elt(a.c, CDT, (((int64_t)b * a.Hkv + kvh) * a.max_blocks + r) * D + tid, m);
+    c = round_to(m, CDT);
+  }
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) {
+    if (g < a.G) {
+      float p = tid < D ? s_q[g][tid] * c : 0.f;
+      p = group_sum<kWave>(p);
+      if (lane == 0) s_red[g][w] = p;
+    }
+  }
+  __syncthreads();
+  if (tid < a.G) {
+    float sc = 0.f;
+#pragma unroll
+    for (int i = 0; i < kNT / kWave; ++i) sc += s_red[tid][i];
+    a.scores[((int64_t)b * a.Hq + kvh * a.G + tid) * a.sp + r] = sc;
+  }
+}
+
+// Scores of every block of every (sequence, KV head) against its G q-heads.
+// 1-D grid: first n_app workgroups per (sequence, KV head) for the appended
+// blocks (dispatched first: their dependent K loads are the longest chain),
+// then n_chunks workgroups per (sequence, KV head) of CB blocks each.  A chunk
+// workgroup stages the G queries through LDS into registers and reads every
+// centroid row once with 16-byte loads, dotting it with all G queries (fp32
+// FMA, then a DPP butterfly over the lanes sharing the row).
 template <int CDT, int D, int GMAX>
 __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
   constexpr int EPV = Elt<CDT>::kPerVec;
@@ -69,71 +113,59 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
   constexpr int CB = (kNT / kWave) * RPW;   // rows (blocks) per workgroup
   __shared__ float s_q[GMAX][D];
   __shared__ float s_sc[GMAX][CB];
+  __shared__ float s_tile[kNT * 8];
+  __shared__ float s_red[GMAX][kNT / kWave];
 
-  const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  int id = blockIdx.x;
+  const bool app = id < a.n_app * a.Hkv * a.B;
+  int unit, kvh, b;
+  if (app) {
+    unit = id % a.n_app; id /= a.n_app;
+  } else {
+    id -= a.n_app * a.Hkv * a.B;
+    unit = id % a.n_chunks; id /= a.n_chunks;
+  }
+  kvh = id % a.Hkv;
+  b = id / a.Hkv;
   const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
   const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
-  const int row0 = chunk * CB;
-  if (row0 >= nb) return;
+  const int first_app = a.n_new > 0 ? max(len - a.n_new, 0) / a.bs : nb;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
-  const int seg = lane % LPR, rsub = lane / LPR;
   const int G = a.G;
+  const int64_t qbase = (int64_t)b * a.qsb + (int64_t)kvh * G * a.qsh;
 
+  if (app) {
+    const int r = first_app + unit;
+    if (r >= nb) return;
+    stage_q<kNT, GMAX, D>(s_q, a.q, a.qdt, qbase, a.qsh, G, 1.f);
+    with_dtype(a.kdt, [&](auto tag) {
+      append_block<CDT, decltype(tag)::value, D, GMAX>(a, b, kvh, r, len, s_q, s_tile, s_red);
+    });
+    return;
+  }
+  const int row0 = unit * CB;
+  const int nrows = min(nb, first_app);     // appended blocks are scored by their own workgroups
+  if (row0 >= nrows) return;
+  const int seg = lane % LPR, rsub = lane / LPR;
   const int64_t cbase_el = (((int64_t)b * a.Hkv + kvh) * a.max_blocks) * D;
   const char* cbase = reinterpret_cast<const char*>(a.c) + cbase_el * EB;
   uint4 cv[NLD];
-  int rows[NLD];
 #pragma unroll
   for (int i = 0; i < NLD; ++i) {
-    rows[i] = row0 + w * RPW + i * RPL + rsub;
-    cv[i] = rows[i] < nb ? load16(cbase + ((int64_t)rows[i] * D + seg * EPV) * EB)
-                         : make_uint4(0, 0, 0, 0);
+    const int r = min(row0 + w * RPW + i * RPL + rsub, nrows - 1);   // in bounds; extra rows unused
+    cv[i] = load16(cbase + ((int64_t)r * D + seg * EPV) * EB);
   }
-  for (int i = tid; i < G * D; i += kNT)
-    s_q[i / D][i % D] = load_elt(a.q, a.qdt, (int64_t)b * a.qsb + (int64_t)(kvh * G + i / D) * a.qsh + i % D);
+  stage_q<kNT, GMAX, D>(s_q, a.q, a.qdt, qbase, a.qsh, G, 1.f);
   __syncthreads();
   float qv[GMAX][EPV];
 #pragma unroll
   for (int g = 0; g < GMAX; ++g)
 #pragma unroll
     for (int e = 0; e < EPV; ++e) qv[g][e] = g < G ? s_q[g][seg * EPV + e] : 0.f;
-
-  const int first_app = a.n_new > 0 ? max(len - a.n_new, 0) / a.bs : nb;
 #pragma unroll
   for (int i = 0; i < NLD; ++i) {
     float x[EPV];
-    const int r = rows[i];
-    if (r >= first_app && r < nb) {
-      // decode-time append: this block gained tokens; its centroid is the
-      // sequential fp32 mean of its real tokens, rounded once to the centroid type
-      const int t0 = r * a.bs, t1 = min(t0 + a.bs, len);
-      const int kbytes = a.kdt == ADAKV_F32 ? 4 : 2;
-      const char* kp = reinterpret_cast<const char*>(a.k) +
-                       ((int64_t)b * a.ksb + (int64_t)kvh * a.ksh + (int64_t)t0 * a.kss + seg * EPV) * kbytes;
-      const int64_t kstep = a.kss * kbytes;
-      float acc[EPV];
-      // the tokens' slices are loaded 8 at a time, then added in token order
-      for (int t = t0; t < t1; t += 8) {
-        float xs[8][EPV];
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (t + u < t1) load_slice<EPV>(kp + (int64_t)(t - t0 + u) * kstep, a.kdt, xs[u]);
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (t + u < t1)
-#pragma unroll
-            for (int e = 0; e < EPV; ++e) acc[e] = t + u == t0 ? xs[u][e] : acc[e] + xs[u][e];
-      }
-      const int64_t crow = cbase_el + (int64_t)r * D + seg * EPV;
-#pragma unroll
-      for (int e = 0; e < EPV; ++e) {
-        const float m = __fdiv_rn(acc[e], (float)(t1 - t0));
-        store_elt(a.c, CDT, crow + e, m);
-        x[e] = round_to(m, CDT);
-      }
-    } else {
-      unpack<CDT>(cv[i], x);
-    }
+    unpack<CDT>(cv[i], x);
 #pragma unroll
     for (int g = 0; g < GMAX; ++g) {
       if (g < G) {
@@ -148,7 +180,7 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
   __syncthreads();
   for (int idx = tid; idx < G * CB; idx += kNT) {
     const int g = idx / CB, r = idx % CB;
-    if (row0 + r < nb)
+    if (row0 + r < nrows)
       a.scores[((int64_t)b * a.Hq + kvh * G + g) * a.sp + row0 + r] = s_sc[g][r];
   }
 }
@@ -499,10 +531,13 @@ __global__ __launch_bounds__(kNT) void budget_kernel(BudgetArgs a) {
 }
 
 template <int CDT, int D>
-hipError_t launch_score_d(const ScoreArgs& a, hipStream_t s) {
+hipError_t launch_score_d(ScoreArgs a, hipStream_t s) {
   constexpr int EPV = Elt<CDT>::kPerVec;
   constexpr int CB = (kNT / kWave) * (kWave / (D / EPV)) * 4;
-  dim3 grid((a.max_blocks + CB - 1) / CB, a.Hkv, a.B);
+  a.n_chunks = (a.max_blocks + CB - 1) / CB;
+  // blocks holding the newest n_new tokens: at most ceil(n_new / bs) + 1
+  a.n_app = a.n_new > 0 ? std::min((a.n_new + a.bs - 1) / a.bs + 1, a.max_blocks) : 0;
+  dim3 grid((unsigned)((int64_t)(a.n_app + a.n_chunks) * a.Hkv * a.B));
   if (a.G <= 1) hipLaunchKernelGGL((score_kernel<CDT, D, 1>), grid, dim3(kNT), 0, s, a);
   else if (a.G <= 2) hipLaunchKernelGGL((score_kernel<CDT, D, 2>), grid, dim3(kNT), 0, s, a);
   else if (a.G <= 4) hipLaunchKernelGGL((score_kernel<CDT, D, 4>), grid, dim3(kNT), 0, s, a);

@@ -206,6 +206,8 @@ def _random_table(rng, Hq, nb, width, lens):
     (8, 4, 4096, 128, 16, torch.bfloat16),
     (2, 8, 1000, 128, 16, torch.bfloat16),      # GQA 8, partial tail block
     (2, 3, 777, 32, 8, torch.float32),
+    (2, 3, 777, 32, 8, torch.bfloat16),         # blocks shorter than a 16-token tile
+    (2, 4, 1500, 64, 24, torch.float16),        # blocks of 1.5 tiles, padded q-heads
     (2, 2, 600, 256, 16, torch.bfloat16),
 ])
 def test_sparse_decode_matches_same_selection_reference(Hkv, group, S, D, bs, dt):
