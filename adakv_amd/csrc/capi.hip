@@ -181,14 +181,20 @@ int run_plan(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_cent
     sa.k = kv_append->k; sa.kdt = kv_append->dtype;
     sa.ksb = kv_append->stride_b; sa.ksh = kv_append->stride_h; sa.kss = kv_append->stride_s;
   }
+  sa.parts = reinterpret_cast<float*>(ws + L.parts);
+  sa.parts_pitch = L.parts_pitch;
+  sa.cfg = budget_cfg(p);
   if (launch_score(sa, c->dtype, g->head_dim, s) != hipSuccess) return ADAKV_ERR_LAUNCH;
   SelectArgs se{};
   se.scores = sa.scores; se.sp = L.sp;
   se.seq_lens = lens; se.uniform_len = g->max_seq_len; se.bs = g->block_size;
   se.B = g->batch; se.Hq = g->n_q_heads;
-  se.cfg = budget_cfg(p);
+  se.cfg = sa.cfg;
   se.table = table; se.T = T;
   se.wbuf = reinterpret_cast<double*>(ws + L.weights);
+  se.parts = sa.parts; se.parts_pitch = sa.parts_pitch;
+  se.n_chunks = sa.n_chunks; se.chunk_rows = sa.chunk_rows;
+  se.n_new = n_new;
   if (launch_select(se, g->max_blocks, s) != hipSuccess) return ADAKV_ERR_LAUNCH;
   if (!sel_lens) return ADAKV_OK;
   BudgetArgs ba{};
@@ -267,6 +273,9 @@ WorkspaceLayout workspace_layout(const adakv_geometry_t& g, int T) {
   off = align_up(off + (size_t)g.batch * g.n_kv_heads * L.nsplit_max * G * (g.head_dim + 2) * 4);
   L.table = off;         off = align_up(off + (size_t)g.batch * g.n_q_heads * T * 4);
   L.lens = off;          off = align_up(off + (size_t)g.batch * g.n_q_heads * 4);
+  L.parts_pitch = score_chunks_max(g.max_blocks, g.head_dim);
+  L.parts = off;
+  off = align_up(off + (size_t)g.batch * g.n_q_heads * L.parts_pitch * kPartFloats * 4);
   L.total = off;
   return L;
 }

@@ -37,8 +37,18 @@ struct ScoreArgs {
   const void* k;
   int kdt;
   int64_t ksb, ksh, kss;
-  int n_app, n_chunks;         // set by the launcher: workgroups per (sequence, KV head)
+  // per-chunk softmax partials of the scores (nullptr: not wanted), one
+  // PartRecord per (sequence, q-head, chunk) at parts[(b * Hq + h) * parts_pitch + chunk]
+  float* parts;
+  int parts_pitch;
+  BudgetCfg cfg;
+  int n_app, n_chunks, chunk_rows;   // set by the launcher
 };
+
+// Softmax partial of one chunk of a head's scores z = score / temperature:
+// m = max z, S = sum exp(z - m), T = sum exp(z - m) * (z - m), and the range
+// [lo, hi] of the chunk's sanitised content scores.  8 floats (32 bytes).
+constexpr int kPartFloats = 8;
 
 struct SelectArgs {
   const float* scores;
@@ -50,6 +60,9 @@ struct SelectArgs {
   int32_t* table;              // [B, Hq, T]
   int T;
   double* wbuf;                // [B, Hq] entropy weights (adaptive policy)
+  const float* parts;          // per-chunk partials written by the score kernel
+  int parts_pitch, n_chunks, chunk_rows;
+  int n_new;                   // rows >= first appended block are not in any chunk partial
 };
 
 struct BudgetArgs {
@@ -103,14 +116,18 @@ struct MergeArgs {
 
 // Workspace layout (all offsets 256-byte aligned).
 struct WorkspaceLayout {
-  size_t scores, weights, counters_plan, counters_dec, partials, table, lens, total;
+  size_t scores, weights, counters_plan, counters_dec, partials, table, lens, parts, total;
+  int parts_pitch;
   int sp, nsplit_sparse, nsplit_dense, nsplit_max;
 };
 
 WorkspaceLayout workspace_layout(const adakv_geometry_t& g, int table_width);
 
 hipError_t launch_centroid(const CentroidArgs& a, int kdt, int cdt, int D, hipStream_t s);
-hipError_t launch_score(const ScoreArgs& a, int cdt, int D, hipStream_t s);
+// Sets a.n_app, a.n_chunks and a.chunk_rows for the chosen kernel.
+hipError_t launch_score(ScoreArgs& a, int cdt, int D, hipStream_t s);
+// Chunks per (sequence, KV head) for any centroid dtype: bound on parts_pitch.
+int score_chunks_max(int max_blocks, int D);
 hipError_t launch_select(const SelectArgs& a, int max_blocks, hipStream_t s);
 hipError_t launch_budget(const BudgetArgs& a, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs& a, int kvdt, int D, hipStream_t s);

@@ -38,6 +38,13 @@ __device__ __forceinline__ float round_to(float x, int dt) {
   return x;
 }
 
+// NaN ranks last, infinities clamp to the finite range (they then tie with
+// +/-FLT_MAX and are ordered by block index).
+__device__ __forceinline__ float sanitize(float x) {
+  if (x != x) return -FLT_MAX;
+  return fminf(fmaxf(x, -FLT_MAX), FLT_MAX);
+}
+
 // ---------------------------------------------------------------- scores ----
 // Decode-time append (adakv/estimator.py:62-74): block r gained tokens, so its
 // centroid becomes the sequential fp32 mean of its real tokens (summed in
@@ -183,6 +190,52 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
     if (row0 + r < nrows)
       a.scores[((int64_t)b * a.Hq + kvh * G + g) * a.sp + row0 + r] = s_sc[g][r];
   }
+  if (a.parts == nullptr) return;
+  // softmax partial of this chunk, one wave per q-head (adakv/budget.py:33-37 is
+  // then finished from the partials by the selection)
+  constexpr int RL = (CB + kWave - 1) / kWave;   // rows per lane
+  const Bounds bb = budget_bounds(nb, a.cfg);
+  const int c_lo = bb.sink, c_hi = nb - bb.local;
+  const float tf = (float)fmax(a.cfg.temperature, 1e-6);
+  for (int g = w; g < G; g += kNT / kWave) {
+    float z[RL];
+    float m = -INFINITY, lo = FLT_MAX, hi = -FLT_MAX;
+#pragma unroll
+    for (int k = 0; k < RL; ++k) {
+      const int r = lane + k * kWave;
+      const bool ok = r < CB && row0 + r < nrows;
+      const float x = ok ? s_sc[g][r] : 0.f;
+      z[k] = ok ? (tf == 1.f ? x : __fdiv_rn(x, tf)) : -INFINITY;
+      m = fmaxf(m, z[k]);
+      if (ok && row0 + r >= c_lo && row0 + r < c_hi) {
+        const float xs = sanitize(x);
+        lo = fminf(lo, xs);
+        hi = fmaxf(hi, xs);
+      }
+    }
+    m = wave_allreduce(m, OpMax());
+    float S = 0.f, T = 0.f;
+    if (m != -INFINITY) {
+#pragma unroll
+      for (int k = 0; k < RL; ++k) {
+        if (z[k] != -INFINITY) {
+          const float e = __expf(z[k] - m);
+          S += e;
+          T = fmaf(e, z[k] - m, T);
+        }
+      }
+    }
+    S = wave_allreduce(S, OpAdd());
+    T = wave_allreduce(T, OpAdd());
+    lo = wave_allreduce(lo, OpMin());
+    hi = wave_allreduce(hi, OpMax());
+    if (lane == 0) {
+      float4* rec = reinterpret_cast<float4*>(a.parts + (((int64_t)b * a.Hq + kvh * G + g) * a.parts_pitch + unit) *
+                                                            kPartFloats);
+      rec[0] = make_float4(m, S, T, lo);
+      rec[1] = make_float4(hi, 0.f, 0.f, 0.f);
+    }
+  }
 }
 
 // ------------------------------------------------------------- selection ----
@@ -195,13 +248,6 @@ __device__ __forceinline__ uint64_t sel_key(float x, int idx) {
 }
 __device__ __forceinline__ int key_index(uint64_t k) {
   return (int)(0xffffffffu - (uint32_t)(k & 0xffffffffu));
-}
-
-// NaN ranks last, infinities clamp to the finite range (they then tie with
-// +/-FLT_MAX and are ordered by block index).
-__device__ __forceinline__ float sanitize(float x) {
-  if (x != x) return -FLT_MAX;
-  return fminf(fmaxf(x, -FLT_MAX), FLT_MAX);
 }
 
 // Bitonic sort of s_keys[0, n) into descending order; n a power of two <= kSortCap.
@@ -239,12 +285,43 @@ __device__ __forceinline__ int popcnt(M m) {
   if constexpr (sizeof(M) == 8) return __popcll(m); else return __popc(m);
 }
 
-// Online-softmax pair (running max, sum of exp relative to it).
-__device__ __forceinline__ void ms_merge(float& m, float& s, float m2, float s2) {
-  const float M = fmaxf(m, m2);
-  if (M == -INFINITY) { m = M; s = 0.f; return; }
-  s = s * __expf(m - M) + s2 * __expf(m2 - M);
-  m = M;
+// Softmax partial (see PartRecord layout) and its merge: the larger max wins,
+// the other side's sums are rescaled by exp(m' - M); T picks up (m' - M) * S'.
+struct Part {
+  float m, S, T, lo, hi;
+};
+__device__ __forceinline__ Part part_empty() { return Part{-INFINITY, 0.f, 0.f, FLT_MAX, -FLT_MAX}; }
+__device__ __forceinline__ Part part_merge(const Part& x, const Part& y) {
+  Part r;
+  r.m = fmaxf(x.m, y.m);
+  r.lo = fminf(x.lo, y.lo);
+  r.hi = fmaxf(x.hi, y.hi);
+  if (r.m == -INFINITY) { r.S = 0.f; r.T = 0.f; return r; }
+  const float dx = x.m - r.m, dy = y.m - r.m;
+  const float fx = x.m == -INFINITY ? 0.f : __expf(dx), fy = y.m == -INFINITY ? 0.f : __expf(dy);
+  r.S = x.S * fx + y.S * fy;
+  r.T = (x.m == -INFINITY ? 0.f : fx * fmaf(dx, x.S, x.T)) + (y.m == -INFINITY ? 0.f : fy * fmaf(dy, y.S, y.T));
+  return r;
+}
+template <int CTRL>
+__device__ __forceinline__ Part part_dpp(const Part& p) {
+  return Part{dpp_mov<CTRL>(p.m), dpp_mov<CTRL>(p.S), dpp_mov<CTRL>(p.T), dpp_mov<CTRL>(p.lo), dpp_mov<CTRL>(p.hi)};
+}
+// Merge over the 64 lanes; every lane receives the result.
+__device__ __forceinline__ Part part_wave_merge(Part p) {
+  p = part_merge(p, part_dpp<0xB1>(p));
+  p = part_merge(p, part_dpp<0x4E>(p));
+  p = part_merge(p, part_dpp<0x141>(p));
+  p = part_merge(p, part_dpp<0x140>(p));
+  {
+    const LanePair a = swap16(p.m), b = swap16(p.S), c = swap16(p.T), d = swap16(p.lo), e = swap16(p.hi);
+    p = part_merge(Part{a.a, b.a, c.a, d.a, e.a}, Part{a.b, b.b, c.b, d.b, e.b});
+  }
+  {
+    const LanePair a = swap32(p.m), b = swap32(p.S), c = swap32(p.T), d = swap32(p.lo), e = swap32(p.hi);
+    p = part_merge(Part{a.a, b.a, c.a, d.a, e.a}, Part{a.b, b.b, c.b, d.b, e.b});
+  }
+  return p;
 }
 
 template <int NT, int IPT>
@@ -255,8 +332,7 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
   constexpr Mask kOne = 1;
   __shared__ uint64_t s_keys[kSortCap];
   __shared__ int s_hist[256];
-  __shared__ float s_r[NW][4];
-  __shared__ float s_h[NW];
+  __shared__ float s_r[NW][5];
   __shared__ float s_f[NW];
   __shared__ int s_i[NW];
   __shared__ int s_bc[4];
@@ -295,68 +371,41 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
     }
   }
 
-  // ---- pass A: softmax (max, sum) of scores / T and the content score range ----
+  // ---- softmax partials: the score kernel's chunks plus rows it left out ----
+  // (blocks recomputed by the decode-time append are scored separately and
+  // belong to no chunk); merged with the same rule at every level.
+  const int first_app = a.n_new > 0 ? max(len - a.n_new, 0) / a.bs : nb;
+  const int rows_in_chunks = min(nb, first_app);
   const float tf = (float)fmax(a.cfg.temperature, 1e-6);
   const bool unit = tf == 1.f;
-  float m = -INFINITY, ssum = 0.f, vlo = FLT_MAX, vhi = -FLT_MAX;
+  Part pt = part_empty();
+  for (int c = tid; c * a.chunk_rows < rows_in_chunks; c += NT) {
+    const float4* rec = reinterpret_cast<const float4*>(a.parts + (((int64_t)b * a.Hq + h) * a.parts_pitch + c) *
+                                                                  kPartFloats);
+    const float4 r0 = rec[0], r1 = rec[1];
+    pt = part_merge(pt, Part{r0.x, r0.y, r0.z, r0.w, r1.x});
+  }
   Mask content = 0;
 #pragma unroll
   for (int i = 0; i < IPT; ++i) {
     const int idx = base + i;
-    if (adaptive && idx < nb) {
+    const bool is_content = idx >= c_lo && idx < c_hi;
+    if (is_content) content |= kOne << i;
+    if (idx >= rows_in_chunks && idx < nb) {
       const float z = unit ? v[i] : __fdiv_rn(v[i], tf);
-      if (z > m) { ssum = ssum * __expf(m - z) + 1.f; m = z; }
-      else ssum += __expf(z - m);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < IPT; ++i) {
-    const int idx = base + i;
-    if (idx >= c_lo && idx < c_hi) {
-      content |= kOne << i;
       const float xs = sanitize(v[i]);
-      vlo = fminf(vlo, xs);
-      vhi = fmaxf(vhi, xs);
+      pt = part_merge(pt, Part{z, 1.f, 0.f, is_content ? xs : FLT_MAX, is_content ? xs : -FLT_MAX});
     }
   }
-  // wave reduction of the (max, sum) pairs, then min / max
-  {
-    float mm = m, ss = ssum;
-    float m2 = dpp_mov<0xB1>(mm), s2 = dpp_mov<0xB1>(ss); ms_merge(mm, ss, m2, s2);
-    m2 = dpp_mov<0x4E>(mm); s2 = dpp_mov<0x4E>(ss); ms_merge(mm, ss, m2, s2);
-    m2 = dpp_mov<0x141>(mm); s2 = dpp_mov<0x141>(ss); ms_merge(mm, ss, m2, s2);
-    m2 = dpp_mov<0x140>(mm); s2 = dpp_mov<0x140>(ss); ms_merge(mm, ss, m2, s2);
-    LanePair pm = swap16(mm), ps = swap16(ss);
-    mm = pm.a; ss = ps.a; ms_merge(mm, ss, pm.b, ps.b);
-    pm = swap32(mm); ps = swap32(ss);
-    mm = pm.a; ss = ps.a; ms_merge(mm, ss, pm.b, ps.b);
-    vlo = wave_allreduce(vlo, OpMin());
-    vhi = wave_allreduce(vhi, OpMax());
-    if (lane == 0) { s_r[w][0] = mm; s_r[w][1] = ss; s_r[w][2] = vlo; s_r[w][3] = vhi; }
-  }
+  pt = part_wave_merge(pt);
+  if (lane == 0) { s_r[w][0] = pt.m; s_r[w][1] = pt.S; s_r[w][2] = pt.T; s_r[w][3] = pt.lo; s_r[w][4] = pt.hi; }
   __syncthreads();
-  m = s_r[0][0]; ssum = s_r[0][1]; vlo = s_r[0][2]; vhi = s_r[0][3];
+  pt = Part{s_r[0][0], s_r[0][1], s_r[0][2], s_r[0][3], s_r[0][4]};
 #pragma unroll
-  for (int ww = 1; ww < NW; ++ww) {
-    ms_merge(m, ssum, s_r[ww][0], s_r[ww][1]);
-    vlo = fminf(vlo, s_r[ww][2]);
-    vhi = fmaxf(vhi, s_r[ww][3]);
-  }
+  for (int ww = 1; ww < NW; ++ww) pt = part_merge(pt, Part{s_r[ww][0], s_r[ww][1], s_r[ww][2], s_r[ww][3], s_r[ww][4]});
+  const float vlo = pt.lo, vhi = pt.hi;
 
-  // ---- pass B: entropy terms (budget.py:33-37) and the score histogram ----
-  if (adaptive) {
-    const float inv = 1.f / ssum;
-    float hs = 0.f;
-#pragma unroll
-    for (int i = 0; i < IPT; ++i) {
-      if (base + i < nb) {
-        const float p = __expf((unit ? v[i] : __fdiv_rn(v[i], tf)) - m) * inv;
-        hs += p * __logf(fmaxf(p, 1e-9f));
-      }
-    }
-    hs = wave_allreduce(hs, OpAdd());
-    if (lane == 0) s_h[w] = hs;
-  }
+  // ---- the score histogram over the content range ----
   // 256 linear bins over [vlo, vhi]; bin 0 holds the largest scores.  The bin
   // is a monotone function of the score, so ranks never cross bins.
   const float width = vhi - vlo;
@@ -370,22 +419,20 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
     }
   }
   __syncthreads();
-  if (w == 0) {
-    if (adaptive && lane == 0) {
-      float hsum = 0.f;
-      for (int ww = 0; ww < NW; ++ww) hsum += s_h[ww];
-      a.wbuf[(int64_t)b * a.Hq + h] = (double)(-hsum) / log((double)max(nb, 2)) + 1e-6;
-    }
-    if (KC > 0) {
-      int c4[4], s4 = 0;
+  if (w == 1 && lane == 0 && adaptive) {
+    // normalised entropy weight (adakv/budget.py:33-37): sum p log p = T / S - log S
+    const float hs = pt.T / pt.S - __logf(pt.S);
+    a.wbuf[(int64_t)b * a.Hq + h] = (double)(-hs) / log((double)max(nb, 2)) + 1e-6;
+  }
+  if (w == 0 && KC > 0) {
+    int c4[4], s4 = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) { c4[j] = s_hist[4 * lane + j]; s4 += c4[j]; }
-      int before = wave_incl_scan(s4) - s4;
+    for (int j = 0; j < 4; ++j) { c4[j] = s_hist[4 * lane + j]; s4 += c4[j]; }
+    int before = wave_incl_scan(s4) - s4;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (before < KC && KC <= before + c4[j]) { s_bc[0] = 4 * lane + j; s_bc[1] = before + c4[j]; }
-        before += c4[j];
-      }
+    for (int j = 0; j < 4; ++j) {
+      if (before < KC && KC <= before + c4[j]) { s_bc[0] = 4 * lane + j; s_bc[1] = before + c4[j]; }
+      before += c4[j];
     }
   }
   __syncthreads();
@@ -531,9 +578,10 @@ __global__ __launch_bounds__(kNT) void budget_kernel(BudgetArgs a) {
 }
 
 template <int CDT, int D>
-hipError_t launch_score_d(ScoreArgs a, hipStream_t s) {
+hipError_t launch_score_d(ScoreArgs& a, hipStream_t s) {
   constexpr int EPV = Elt<CDT>::kPerVec;
   constexpr int CB = (kNT / kWave) * (kWave / (D / EPV)) * 4;
+  a.chunk_rows = CB;
   a.n_chunks = (a.max_blocks + CB - 1) / CB;
   // blocks holding the newest n_new tokens: at most ceil(n_new / bs) + 1
   a.n_app = a.n_new > 0 ? std::min((a.n_new + a.bs - 1) / a.bs + 1, a.max_blocks) : 0;
@@ -546,7 +594,7 @@ hipError_t launch_score_d(ScoreArgs a, hipStream_t s) {
 }
 
 template <int CDT>
-hipError_t launch_score_c(const ScoreArgs& a, int D, hipStream_t s) {
+hipError_t launch_score_c(ScoreArgs& a, int D, hipStream_t s) {
   switch (D) {
     case 32: return launch_score_d<CDT, 32>(a, s);
     case 64: return launch_score_d<CDT, 64>(a, s);
@@ -558,7 +606,13 @@ hipError_t launch_score_c(const ScoreArgs& a, int D, hipStream_t s) {
 
 }  // namespace
 
-hipError_t launch_score(const ScoreArgs& a, int cdt, int D, hipStream_t s) {
+int score_chunks_max(int max_blocks, int D) {
+  // the smallest chunk is that of fp32 centroids: 16 rows per wave-wide load set
+  const int cb = std::max(1, (kNT / kWave) * (kWave / std::max(1, D / 4)) * 4);
+  return (max_blocks + cb - 1) / cb;
+}
+
+hipError_t launch_score(ScoreArgs& a, int cdt, int D, hipStream_t s) {
   switch (cdt) {
     case ADAKV_F32: return launch_score_c<ADAKV_F32>(a, D, s);
     case ADAKV_F16: return launch_score_c<ADAKV_F16>(a, D, s);
