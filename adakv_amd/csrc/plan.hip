@@ -324,6 +324,30 @@ __device__ __forceinline__ Part part_wave_merge(Part p) {
   return p;
 }
 
+// Normalised entropy weight of head h (adakv/budget.py:33-37), by one wave
+// from the per-wave softmax partials: sum p log p = T / S - log S.
+template <int NW>
+__device__ __forceinline__ void write_weight(const SelectArgs& a, int b, int h, int nb, bool adaptive,
+                                             const float (*s_r)[5]) {
+  if (!adaptive) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const bool ok = lane < NW;
+  const float m = ok ? s_r[lane][0] : -INFINITY;
+  const float M = wave_allreduce(m, OpMax());
+  float S = 0.f, T = 0.f;
+  if (m != -INFINITY) {
+    const float d = m - M, f = __expf(d);
+    S = s_r[lane][1] * f;
+    T = f * fmaf(d, s_r[lane][1], s_r[lane][2]);
+  }
+  S = wave_allreduce(S, OpAdd());
+  T = wave_allreduce(T, OpAdd());
+  if (lane == 0) {
+    const float hs = T / S - __logf(S);
+    a.wbuf[(int64_t)b * a.Hq + h] = (double)(-hs) / log((double)max(nb, 2)) + 1e-6;
+  }
+}
+
 template <int NT, int IPT>
 __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
   static_assert(IPT <= 64 && IPT % 4 == 0 && NT >= 256, "one mask word per thread");
@@ -333,6 +357,10 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
   __shared__ uint64_t s_keys[kSortCap];
   __shared__ int s_hist[256];
   __shared__ float s_r[NW][5];
+  __shared__ int s_rank[kSortCap];
+  __shared__ float s_max[NT];             // chunk content maxima (+ appended rows)
+  __shared__ float s_tau;
+  __shared__ int s_mrank[NT];
   __shared__ float s_f[NW];
   __shared__ int s_i[NW];
   __shared__ int s_bc[4];
@@ -347,8 +375,9 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
   const int n_content = max(c_hi - c_lo, 0);
   const int KC = min(max(bb.kcap - bb.n_forced, 0), n_content);
   const bool adaptive = a.cfg.policy == ADAKV_POLICY_ADAPTIVE && nb > 1;
-  if (tid < 256) s_hist[tid] = 0;
-  if (tid == 0) s_n = 0;
+  if (tid == 0) { s_n = 0; s_tau = -FLT_MAX; }
+  for (int i = tid; i < kSortCap; i += NT) s_rank[i] = 0;
+  s_mrank[tid] = 0;
 
   // ---- forced prefix and padding of the block-table row ----
   int32_t* trow = a.table + ((int64_t)b * a.Hq + h) * a.T;
@@ -371,19 +400,25 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
     }
   }
 
-  // ---- softmax partials: the score kernel's chunks plus rows it left out ----
-  // (blocks recomputed by the decode-time append are scored separately and
-  // belong to no chunk); merged with the same rule at every level.
+  // ---- softmax partials: the score kernel's chunks plus the rows it left out ----
+  // (blocks recomputed by the decode-time append are scored on their own and
+  // belong to no chunk; each counts as a one-row chunk here).  A wave first
+  // takes the max, rescales its lanes' sums to it once, then adds.
   const int first_app = a.n_new > 0 ? max(len - a.n_new, 0) / a.bs : nb;
   const int rows_in_chunks = min(nb, first_app);
+  const int n_chunks = ceil_div(rows_in_chunks, a.chunk_rows);
   const float tf = (float)fmax(a.cfg.temperature, 1e-6);
   const bool unit = tf == 1.f;
   Part pt = part_empty();
-  for (int c = tid; c * a.chunk_rows < rows_in_chunks; c += NT) {
+  bool has = false;
+  for (int c = tid; c < n_chunks; c += NT) {
     const float4* rec = reinterpret_cast<const float4*>(a.parts + (((int64_t)b * a.Hq + h) * a.parts_pitch + c) *
                                                                   kPartFloats);
     const float4 r0 = rec[0], r1 = rec[1];
     pt = part_merge(pt, Part{r0.x, r0.y, r0.z, r0.w, r1.x});
+    // content maximum of the chunk (none: -inf); chunks past NT are not counted
+    if (c < NT) s_max[c] = (r1.x == -FLT_MAX && r0.w == FLT_MAX) ? -INFINITY : r1.x;
+    has = true;
   }
   Mask content = 0;
 #pragma unroll
@@ -395,65 +430,91 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
       const float z = unit ? v[i] : __fdiv_rn(v[i], tf);
       const float xs = sanitize(v[i]);
       pt = part_merge(pt, Part{z, 1.f, 0.f, is_content ? xs : FLT_MAX, is_content ? xs : -FLT_MAX});
+      const int t = n_chunks + idx - rows_in_chunks;
+      if (t < NT) s_max[t] = is_content ? xs : -INFINITY;
+      has = true;
     }
   }
-  pt = part_wave_merge(pt);
+  const int n_max = min(n_chunks + (nb - rows_in_chunks), NT);
+  if (__ballot(has) != 0) {                    // waves without partials skip the reductions
+    const float M = wave_allreduce(pt.m, OpMax());
+    float S = 0.f, T = 0.f;
+    if (pt.m != -INFINITY) {
+      const float d = pt.m - M, f = __expf(d);
+      S = pt.S * f;
+      T = f * fmaf(d, pt.S, pt.T);
+    }
+    pt = Part{M, wave_allreduce(S, OpAdd()), wave_allreduce(T, OpAdd()), wave_allreduce(pt.lo, OpMin()),
+              wave_allreduce(pt.hi, OpMax())};
+  }
   if (lane == 0) { s_r[w][0] = pt.m; s_r[w][1] = pt.S; s_r[w][2] = pt.T; s_r[w][3] = pt.lo; s_r[w][4] = pt.hi; }
   __syncthreads();
-  pt = Part{s_r[0][0], s_r[0][1], s_r[0][2], s_r[0][3], s_r[0][4]};
-#pragma unroll
-  for (int ww = 1; ww < NW; ++ww) pt = part_merge(pt, Part{s_r[ww][0], s_r[ww][1], s_r[ww][2], s_r[ww][3], s_r[ww][4]});
-  const float vlo = pt.lo, vhi = pt.hi;
-
-  // ---- the score histogram over the content range ----
-  // 256 linear bins over [vlo, vhi]; bin 0 holds the largest scores.  The bin
-  // is a monotone function of the score, so ranks never cross bins.
-  const float width = vhi - vlo;
-  const float binv = (width > 0.f && width <= FLT_MAX) ? 256.f / width : 0.f;
-  auto bin_of = [&](float x) { return (int)fminf(255.f, floorf((vhi - x) * binv)); };
-#pragma unroll
-  for (int i = 0; i < IPT; ++i) {
-    if ((content >> i) & kOne) {
-      v[i] = sanitize(v[i]);
-      if (KC > 0) atomicAdd(&s_hist[bin_of(v[i])], 1);
-    }
-  }
-  __syncthreads();
-  if (w == 1 && lane == 0 && adaptive) {
-    // normalised entropy weight (adakv/budget.py:33-37): sum p log p = T / S - log S
-    const float hs = pt.T / pt.S - __logf(pt.S);
-    a.wbuf[(int64_t)b * a.Hq + h] = (double)(-hs) / log((double)max(nb, 2)) + 1e-6;
-  }
-  if (w == 0 && KC > 0) {
-    int c4[4], s4 = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) { c4[j] = s_hist[4 * lane + j]; s4 += c4[j]; }
-    int before = wave_incl_scan(s4) - s4;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (before < KC && KC <= before + c4[j]) { s_bc[0] = 4 * lane + j; s_bc[1] = before + c4[j]; }
-      before += c4[j];
-    }
-  }
-  __syncthreads();
-  if (KC <= 0) return;
-
-  const int bstar = s_bc[0], n_cand = s_bc[1];
-  if (n_cand <= kSortCap) {
-    // candidates: every content block in bins <= b*; rank them exactly
-#pragma unroll
-    for (int i = 0; i < IPT; ++i)
-      if (((content >> i) & kOne) && bin_of(v[i]) <= bstar) s_keys[atomicAdd(&s_n, 1)] = sel_key(v[i], base + i);
-    __syncthreads();
-    const int n = s_n;
-    for (int i = tid; i < n; i += NT) {
-      const uint64_t ki = s_keys[i];
-      int rank = 0;
-      for (int j = 0; j < n; ++j) rank += s_keys[j] > ki;
-      if (rank < KC) trow[bb.n_forced + rank] = key_index(ki);
-    }
+  if (KC <= 0) {
+    if (w == NW - 1) write_weight<NW>(a, b, h, nb, adaptive, s_r);
     return;
   }
+
+  // ---- selection threshold tau: the KC-th largest chunk content maximum ----
+  // At least KC content scores (those maxima) are >= tau, so every one of the
+  // top KC is; missing maxima only lower tau.  Ranks of the maxima are
+  // counted with the pairs spread over the workgroup.
+  if (n_max >= KC) {
+    const int npad = next_pow2(max(n_max, 1));
+    const int parts = max(NT / npad, 1), jlen = ceil_div(n_max, parts);
+    const int i = tid % npad, j0 = (tid / npad) * jlen, j1 = min(n_max, j0 + jlen);
+    if (i < n_max && tid / npad < parts) {
+      const float x = s_max[i];
+      int r = 0;
+      for (int j = j0; j < j1; ++j) {
+        const float y = s_max[j];
+        r += (y > x) || (y == x && j < i);
+      }
+      if (r) atomicAdd(&s_mrank[i], r);
+    }
+    __syncthreads();
+    for (int i2 = tid; i2 < n_max; i2 += NT)
+      if (s_mrank[i2] == KC - 1) s_tau = s_max[i2] == -INFINITY ? -FLT_MAX : s_max[i2];
+  }
+  __syncthreads();
+
+  // ---- candidates: content scores >= tau, compacted wave by wave ----
+  const float tau = s_tau;
+  const bool exact_low = tau == -FLT_MAX;      // compare sanitised scores only at the bottom of the range
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const bool c = ((content >> i) & kOne) && (exact_low ? sanitize(v[i]) >= tau : v[i] >= tau);
+    const uint64_t bal = __ballot(c);
+    if (bal) {
+      int o0 = 0;
+      if (lane == 0) o0 = atomicAdd(&s_n, __popcll(bal));
+      o0 = __shfl(o0, 0);
+      const int o = o0 + __popcll(bal & ((1ull << lane) - 1ull));
+      if (c && o < kSortCap) s_keys[o] = sel_key(sanitize(v[i]), base + i);
+    }
+  }
+  __syncthreads();
+  const int n_cand = s_n;
+  if (n_cand <= kSortCap) {
+    // rank every candidate against all others, the pairs spread over the workgroup
+    const int npad = next_pow2(max(n_cand, 1));
+    const int parts = max(NT / npad, 1), jlen = ceil_div(n_cand, parts);
+    const int i = tid % npad, j0 = (tid / npad) * jlen, j1 = min(n_cand, j0 + jlen);
+    if (i < n_cand && tid / npad < parts) {
+      const uint64_t ki = s_keys[i];
+      int r = 0;
+      for (int j = j0; j < j1; ++j) r += s_keys[j] > ki;
+      if (r) atomicAdd(&s_rank[i], r);
+    }
+    __syncthreads();
+    for (int e = tid; e < n_cand; e += NT)
+      if (s_rank[e] < KC) trow[bb.n_forced + s_rank[e]] = key_index(s_keys[e]);
+    if (w == NW - 1) write_weight<NW>(a, b, h, nb, adaptive, s_r);
+    return;
+  }
+  if (w == NW - 1) write_weight<NW>(a, b, h, nb, adaptive, s_r);
+#pragma unroll
+  for (int i = 0; i < IPT; ++i)
+    if ((content >> i) & kOne) v[i] = sanitize(v[i]);
 
   // ---- fallback: the boundary bin holds too many blocks; refine exactly ----
   Mask cand = content, sel = 0;
