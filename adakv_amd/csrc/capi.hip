@@ -127,7 +127,7 @@ size_t decode_lds_bytes(const adakv_geometry_t& g, int kvdt, int list_cap, bool 
   const int GM = gmax_of(g.n_q_heads / g.n_kv_heads);
   const size_t stat = decode_static_lds(kvdt, g.head_dim, GM, sparse);
   const size_t dyn = sparse ? ((size_t)g.n_q_heads * 8 + 15) / 16 * 16 +
-                                  (size_t)(((g.max_blocks + 3) / 4) + list_cap) * 4
+                                  (size_t)(((g.max_blocks + 3) / 4 + 3) / 4 * 4 + list_cap) * 4
                             : 16;
   return stat + dyn;
 }
@@ -212,7 +212,7 @@ int run_plan(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_cent
 int run_decode(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
                const int32_t* lens, const int32_t* table, int T, const int32_t* sel_lens,
                const adakv_budget_t* p, int32_t* sel_lens_out, float sm_scale,
-               const adakv_output_t* out, char* ws, int T_layout, hipStream_t s) {
+               const adakv_output_t* out, char* ws, int T_layout, bool table_unique, hipStream_t s) {
   const WorkspaceLayout L = workspace_layout(*g, T_layout);
   DecodeArgs d{};
   d.q = q->data; d.qdt = q->dtype; d.qsb = q->stride_b; d.qsh = q->stride_h;
@@ -229,9 +229,16 @@ int run_decode(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv
   d.counters = reinterpret_cast<int*>(ws + L.counters_dec);
   d.max_blocks = g->max_blocks;
   if (table) {
-    d.nsplit = L.nsplit_sparse;
+    // Sparse: one workgroup group per q-head when the hand-off counters allow
+    // (each head streams only its own blocks, so a KV head's union is spread
+    // over G workgroups instead of one); per KV head otherwise.
+    d.per_head = (int64_t)g->batch * g->n_q_heads <= kMaxDecodeCounters;
+    d.table_unique = table_unique;
+    const int64_t umax = d.per_head ? std::min<int64_t>(T, g->max_blocks) : union_max(*g, T);
+    d.nsplit = (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div_h(umax, kSparseMinPer), kMaxSparseSplits));
     d.min_per = kSparseMinPer;
-    d.list_cap = list_cap_of(*g, T, d.nsplit);
+    d.list_cap = (int)std::max<int64_t>(1, std::max<int64_t>(ceil_div_h(umax, d.nsplit),
+                                                             std::min<int64_t>(kSparseMinPer, umax)));
     d.merge_in_kernel = 1;
   } else {
     d.nsplit = L.nsplit_dense;
@@ -369,7 +376,7 @@ int adakv_sparse_decode(const adakv_geometry_t* g, const adakv_query_t* q, const
   if ((st = check_ws(g, sel->table_width, ws, ws_bytes))) return st;
   return run_decode(g, q, kv, seq_lens, sel->block_table, sel->table_width, sel->sel_lens,
                     nullptr, nullptr, sm_scale, out, reinterpret_cast<char*>(ws),
-                    sel->table_width, (hipStream_t)stream);
+                    sel->table_width, false, (hipStream_t)stream);
 }
 
 int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
@@ -398,7 +405,8 @@ int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const 
   const hipStream_t s = (hipStream_t)stream;
   if (append_new > 0 && !centroid_pair_ok(kv->dtype, c->dtype)) return ADAKV_ERR_DTYPE;
   if ((st = run_plan(g, q, c, kv, append_new, seq_lens, p, table, Tl, nullptr, w, s))) return st;
-  return run_decode(g, q, kv, seq_lens, table, Tl, nullptr, p, lens, sm_scale, out, w, Tl, s);
+  // the selection kernel lists distinct valid blocks: no union needed per head
+  return run_decode(g, q, kv, seq_lens, table, Tl, nullptr, p, lens, sm_scale, out, w, Tl, true, s);
 }
 
 int adakv_dense_decode(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
@@ -411,7 +419,7 @@ int adakv_dense_decode(const adakv_geometry_t* g, const adakv_query_t* q, const 
   if (!isfinite(sm_scale)) return ADAKV_ERR_VALUE;
   if ((st = check_ws(g, 1, ws, ws_bytes))) return st;
   return run_decode(g, q, kv, seq_lens, nullptr, 0, nullptr, nullptr, nullptr, sm_scale, out,
-                    reinterpret_cast<char*>(ws), 1, (hipStream_t)stream);
+                    reinterpret_cast<char*>(ws), 1, false, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -12,6 +12,7 @@
 namespace adakv {
 
 constexpr int kWave = 64;
+constexpr int kMaxBlocksDev = 32768;     // largest max_blocks the kernels are built for
 
 // ---- element types ---------------------------------------------------------
 // 16-byte vectors carry 4 fp32 or 8 fp16/bf16 elements.
@@ -191,15 +192,25 @@ __device__ __forceinline__ float wave_min(float x) {
   return x;
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave.
+// Inclusive prefix sum over the 64 lanes of a wave: a Hillis-Steele scan
+// inside each 16-lane row with DPP row shifts (lanes shifted in from outside
+// the row read 0), then the totals of the lower rows added from lanes 15, 31
+// and 47.  No LDS traffic.
+template <int CTRL>
+__device__ __forceinline__ int dpp_row_shr(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
+}
 __device__ __forceinline__ int wave_incl_scan(int x) {
   const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  return x;
+  x += dpp_row_shr<0x111>(x);
+  x += dpp_row_shr<0x112>(x);
+  x += dpp_row_shr<0x114>(x);
+  x += dpp_row_shr<0x118>(x);
+  const int r0 = __builtin_amdgcn_readlane(x, 15);
+  const int r1 = __builtin_amdgcn_readlane(x, 31);
+  const int r2 = __builtin_amdgcn_readlane(x, 47);
+  const int row = lane >> 4;
+  return x + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
 }
 
 // ---- workgroup reductions (NT threads, scratch of >= NT/64 slots) ------------

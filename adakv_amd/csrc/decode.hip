@@ -55,18 +55,54 @@ struct Slice {
   int U, lo, hi, n_active;
 };
 
+// The q-heads a workgroup serves: the G heads of one KV head, or (sparse
+// per-head mode) a single q-head, which then reads its own selection only.
+struct Grp {
+  int unit;   // group index within the sequence
+  int ng;     // groups per sequence
+  int G;      // q-heads in the group
+  int h0;     // first q-head of the group
+  int kv;     // KV head the group reads
+};
+__device__ __forceinline__ Grp group_of(const DecodeArgs& a, int x) {
+  if (a.per_head) return Grp{x, a.Hq, 1, x, x / a.G};
+  return Grp{x, a.Hkv, a.G, x * a.G, x};
+}
+
+// Dynamic LDS of the sparse mode: fp64 weights [Hq], the union bitmap (one
+// byte of head bits per block, rounded up to whole 16-byte quads), the list.
+__device__ __forceinline__ int bitmap_words(int max_blocks) { return ceil_div(ceil_div(max_blocks, 4), 4) * 4; }
+__device__ __forceinline__ uint32_t* bitmap_base(const DecodeArgs& a, unsigned char* s_dyn_raw) {
+  return reinterpret_cast<uint32_t*>(s_dyn_raw + ((a.Hq * 8 + 15) / 16) * 16);
+}
 __device__ __forceinline__ uint32_t* list_base(const DecodeArgs& a, unsigned char* s_dyn_raw) {
-  return reinterpret_cast<uint32_t*>(s_dyn_raw + ((a.Hq * 8 + 15) / 16) * 16) + ceil_div(a.max_blocks, 4);
+  return bitmap_base(a, s_dyn_raw) + bitmap_words(a.max_blocks);
+}
+
+// Bit 4k + i of the result is set when byte i of word k of the quad is non-zero.
+__device__ __forceinline__ uint32_t nonzero_bytes(uint32_t x) {
+  x |= x >> 4;
+  x |= x >> 2;
+  x |= x >> 1;
+  x &= 0x01010101u;
+  return (x | (x >> 7) | (x >> 14) | (x >> 21)) & 0xfu;
+}
+__device__ __forceinline__ uint32_t quad_mask(const uint4& q) {
+  return nonzero_bytes(q.x) | (nonzero_bytes(q.y) << 4) | (nonzero_bytes(q.z) << 8) | (nonzero_bytes(q.w) << 12);
 }
 
 template <int NT>
-__device__ Slice build_slice(const DecodeArgs& a, int b, int kvh, int split, int nb,
+__device__ Slice build_slice(const DecodeArgs& a, int b, const Grp& gr, int split, int nb,
                              unsigned char* s_dyn_raw, int* s_cnt, int* s_misc) {
-  const int tid = threadIdx.x, G = a.G;
+  const int tid = threadIdx.x, G = gr.G;
   double* s_w = reinterpret_cast<double*>(s_dyn_raw);
-  uint32_t* s_bits = reinterpret_cast<uint32_t*>(s_dyn_raw + ((a.Hq * 8 + 15) / 16) * 16);
+  uint32_t* s_bits = bitmap_base(a, s_dyn_raw);
+  uint4* s_quads = reinterpret_cast<uint4*>(s_bits);
   uint32_t* s_list = list_base(a, s_dyn_raw);
-  int U = nb, off = 0, w0 = 0, w1 = 0;
+  // bitmap quads (16 blocks each) owned by this thread: [q0, q0 + qpt)
+  const int nquads = ceil_div(nb, 16);
+  const int qpt = ceil_div(nquads, NT), q0 = tid * qpt, q1 = min(q0 + qpt, nquads);
+  int U = nb, off = 0;
   if (a.table != nullptr) {
     // The table entries that can be selected are loaded up front (before the
     // counts are known); the counts then decide which of them enter the union.
@@ -74,28 +110,47 @@ __device__ Slice build_slice(const DecodeArgs& a, int b, int kvh, int split, int
     const bool derive = a.sel_lens == nullptr;
     const bool adaptive = derive && a.cfg.policy == ADAKV_POLICY_ADAPTIVE && nb > 1;
     const int width = derive ? min(a.T, max(bb.kcap, 0)) : a.T;
-    const int nwords = ceil_div(nb, 4);
     constexpr int EPT = 4;                       // table entries per thread
     int ent[EPT];
 #pragma unroll
     for (int u = 0; u < EPT; ++u) {
       const int e = min(tid + u * NT, max(G * width - 1, 0));   // in bounds; extra entries unused
-      ent[u] = a.table[((int64_t)b * a.Hq + kvh * G + e / width) * a.T + e % width];
+      ent[u] = a.table[((int64_t)b * a.Hq + gr.h0 + e / width) * a.T + e % width];
     }
-    for (int i = tid; i < nwords; i += NT) s_bits[i] = 0;
+    // a single head whose listed blocks are known distinct needs no union:
+    // its list is the valid prefix of its own table row
+    const bool direct = a.table_unique && G == 1 && width <= NT;
+    if (!direct)
+      for (int i = tid; i < nquads; i += NT) s_quads[i] = make_uint4(0, 0, 0, 0);
     if (adaptive)
       for (int h = tid; h < a.Hq; h += NT) s_w[h] = a.wbuf[(int64_t)b * a.Hq + h];
-    if (!derive && tid < G) s_cnt[tid] = min(max(a.sel_lens[(int64_t)b * a.Hq + kvh * G + tid], 0), a.T);
+    if (!derive && tid < G) s_cnt[tid] = min(max(a.sel_lens[(int64_t)b * a.Hq + gr.h0 + tid], 0), a.T);
     __syncthreads();
     if (derive) {
-      // every thread evaluates the same sum of weights in NumPy's order
-      const double wsum = adaptive ? numpy_pairwise_sum<6>(s_w, a.Hq) : 0.0;
-      if (tid < G) {
-        const int k = head_count(bb, a.cfg.policy, adaptive ? s_w[kvh * G + tid] : 0.0, wsum, a.Hq);
-        s_cnt[tid] = min(k, a.T);
-        if (split == 0 && a.sel_lens_out) a.sel_lens_out[(int64_t)b * a.Hq + kvh * G + tid] = k;
+      if (tid < kWave) {
+        // one wave evaluates the sum of weights in NumPy's order
+        const double wsum = adaptive ? numpy_pairwise_sum<6>(s_w, a.Hq) : 0.0;
+        if (tid < G) {
+          const int k = head_count(bb, a.cfg.policy, adaptive ? s_w[gr.h0 + tid] : 0.0, wsum, a.Hq);
+          s_cnt[tid] = min(k, a.T);
+          if (split == 0 && a.sel_lens_out) a.sel_lens_out[(int64_t)b * a.Hq + gr.h0 + tid] = k;
+        }
       }
       __syncthreads();
+    }
+    if (direct) {
+      const int blk = ent[0];
+      const bool ok = tid < s_cnt[0] && blk >= 0 && blk < nb;
+      off = block_excl_scan<NT>(ok ? 1 : 0, s_misc, &U);
+      Slice r;
+      r.U = U;
+      const int per = U > 0 ? max(ceil_div(U, a.nsplit), a.min_per) : 0;
+      r.n_active = U > 0 ? ceil_div(U, per) : 0;
+      r.lo = split * per;
+      r.hi = min(U, r.lo + per);
+      if (ok && off >= r.lo && off < r.hi) s_list[off - r.lo] = (uint32_t)blk | (1u << 24);
+      __syncthreads();
+      return r;
     }
 #pragma unroll
     for (int u = 0; u < EPT; ++u) {
@@ -107,18 +162,13 @@ __device__ Slice build_slice(const DecodeArgs& a, int b, int kvh, int split, int
     }
     for (int e = EPT * NT + tid; e < G * width; e += NT) {   // tables wider than EPT*NT/G
       const int g = e / width, j = e % width;
-      const int blk = a.table[((int64_t)b * a.Hq + kvh * G + g) * a.T + j];
+      const int blk = a.table[((int64_t)b * a.Hq + gr.h0 + g) * a.T + j];
       if (j < s_cnt[g] && blk >= 0 && blk < nb) atomicOr(&s_bits[blk >> 2], 1u << ((blk & 3) * 8 + g));
     }
     __syncthreads();
-    const int wpt = ceil_div(nwords, NT);
-    w0 = min(tid * wpt, nwords);
-    w1 = min(w0 + wpt, nwords);
     int cnt = 0;
-    for (int i = w0; i < w1; ++i) {
-      const uint32_t x = s_bits[i];
-      cnt += ((x & 0xffu) != 0) + ((x & 0xff00u) != 0) + ((x & 0xff0000u) != 0) + ((x >> 24) != 0);
-    }
+#pragma nounroll
+    for (int qi = q0; qi < q1; ++qi) cnt += __popc(quad_mask(s_quads[qi]));
     off = block_excl_scan<NT>(cnt, s_misc, &U);
   }
   Slice r;
@@ -128,16 +178,19 @@ __device__ Slice build_slice(const DecodeArgs& a, int b, int kvh, int split, int
   r.lo = split * per;
   r.hi = min(U, r.lo + per);
   if (a.table != nullptr && r.lo < r.hi) {
+    // list entries in block order: block id | head mask << 24
     int p = off;
-    for (int i = w0; i < w1; ++i) {
-      const uint32_t x = s_bits[i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t m8 = (x >> (8 * j)) & 0xffu;
-        if (m8) {
-          if (p >= r.lo && p < r.hi) s_list[p - r.lo] = (uint32_t)(4 * i + j) | (m8 << 24);
-          ++p;
-        }
+#pragma nounroll
+    for (int qi = q0; qi < q1 && p < r.hi; ++qi) {
+      const uint4 q = s_quads[qi];
+      uint32_t m = quad_mask(q);
+      while (m) {
+        const int j = __builtin_ctz(m);
+        m &= m - 1;
+        const uint32_t wd = j < 8 ? (j < 4 ? q.x : q.y) : (j < 12 ? q.z : q.w);
+        if (p >= r.lo && p < r.hi)
+          s_list[p - r.lo] = (uint32_t)(16 * qi + j) | (((wd >> (8 * (j & 3))) & 0xffu) << 24);
+        ++p;
       }
     }
   }
@@ -146,11 +199,11 @@ __device__ Slice build_slice(const DecodeArgs& a, int b, int kvh, int split, int
 }
 
 // Block id and head mask of entry e (slice-relative) of the list.
-__device__ __forceinline__ void list_entry(const DecodeArgs& a, const uint32_t* s_list, int lo, int e,
-                                           int& blk, uint32_t& hm) {
+__device__ __forceinline__ void list_entry(const DecodeArgs& a, const Grp& gr, const uint32_t* s_list, int lo,
+                                           int e, int& blk, uint32_t& hm) {
   if (a.table == nullptr) {
     blk = lo + e;
-    hm = (1u << a.G) - 1u;
+    hm = (1u << gr.G) - 1u;
   } else {
     const uint32_t ent = s_list[e];
     blk = (int)(ent & 0xffffffu);
@@ -158,10 +211,10 @@ __device__ __forceinline__ void list_entry(const DecodeArgs& a, const uint32_t* 
   }
 }
 
-__device__ __forceinline__ void write_nan_outputs(const DecodeArgs& a, int b, int kvh, int D, int NT) {
+__device__ __forceinline__ void write_nan_outputs(const DecodeArgs& a, int b, const Grp& gr, int D, int NT) {
   // no valid block for any head of the group: 0/0, as the reference kernel
-  for (int i = threadIdx.x; i < a.G * D; i += NT)
-    store_elt(a.out, a.odt, (int64_t)b * a.osb + (int64_t)(kvh * a.G + i / D) * a.osh + i % D,
+  for (int i = threadIdx.x; i < gr.G * D; i += NT)
+    store_elt(a.out, a.odt, (int64_t)b * a.osb + (int64_t)(gr.h0 + i / D) * a.osh + i % D,
               __builtin_nanf(""));
 }
 
@@ -173,12 +226,12 @@ __device__ __forceinline__ void write_nan_outputs(const DecodeArgs& a, int b, in
 // arrive merges all partials.
 // ---------------------------------------------------------------------------
 template <int NT, int D, int GMAX, int HC, typename Stage>
-__device__ void finish(const DecodeArgs& a, int b, int kvh, int split, const Slice& sl,
+__device__ void finish(const DecodeArgs& a, int b, const Grp& gr, int split, const Slice& sl,
                        float (*s_m)[GMAX], float (*s_l)[GMAX], float (*s_acc)[HC][D], int* s_misc,
                        Stage stage) {
   constexpr int NW = NT / kWave;
-  const int tid = threadIdx.x, G = a.G;
-  float* part = a.partials + (((int64_t)b * a.Hkv + kvh) * a.nsplit) * G * (D + 2);
+  const int tid = threadIdx.x, G = gr.G;
+  float* part = a.partials + (((int64_t)b * gr.ng + gr.unit) * a.nsplit) * G * (D + 2);
   const int64_t pstride = (int64_t)G * (D + 2);
 #pragma unroll
   for (int g0 = 0; g0 < GMAX; g0 += HC) {
@@ -201,7 +254,7 @@ __device__ void finish(const DecodeArgs& a, int b, int kvh, int split, const Sli
         }
       }
       if (sl.n_active == 1) {
-        store_elt(a.out, a.odt, (int64_t)b * a.osb + (int64_t)(kvh * G + g) * a.osh + d, O / L);
+        store_elt(a.out, a.odt, (int64_t)b * a.osb + (int64_t)(gr.h0 + g) * a.osh + d, O / L);
       } else {
         float* pg = part + split * pstride + g * (D + 2);
         pg[2 + d] = O;
@@ -215,7 +268,7 @@ __device__ void finish(const DecodeArgs& a, int b, int kvh, int split, const Sli
   // sparse: the last active slice merges (at most nsplit <= 16 of them)
   __threadfence();
   __syncthreads();
-  if (tid == 0) s_misc[NW] = arrive(&a.counters[(int64_t)b * a.Hkv + kvh]) == sl.n_active - 1;
+  if (tid == 0) s_misc[NW] = arrive(&a.counters[(int64_t)b * gr.ng + gr.unit]) == sl.n_active - 1;
   __syncthreads();
   if (!s_misc[NW]) return;
   __threadfence();
@@ -242,40 +295,56 @@ __device__ void finish(const DecodeArgs& a, int b, int kvh, int split, const Sli
         O += os[sp] * f;
       }
     }
-    store_elt(a.out, a.odt, (int64_t)b * a.osb + (int64_t)(kvh * G + g) * a.osh + d, O / L);
+    store_elt(a.out, a.odt, (int64_t)b * a.osb + (int64_t)(gr.h0 + g) * a.osh + d, O / L);
   }
-  if (tid == 0) reset_counter(&a.counters[(int64_t)b * a.Hkv + kvh]);
+  if (tid == 0) reset_counter(&a.counters[(int64_t)b * gr.ng + gr.unit]);
 }
 
-// Streams items j = w, w + NW, ... of a slice with one item in flight while
-// the previous one is computed.  item(j, t_lo, t_hi, hm) describes item j,
-// load(t_lo, t_hi, bufs...) issues its loads, compute(t_lo, t_hi, hm, bufs...)
-// consumes them.
+// Streams items j = w, w + NW, ... of a slice with two items in flight: the
+// next item's loads are outstanding while the current one is computed, and a
+// buffer is refilled right after its compute.  item(j, t_lo, t_hi, hm)
+// describes item j, load(t_lo, t_hi, buf) issues its loads, compute(t_lo,
+// t_hi, hm, buf) consumes them.  Look-ahead loads are issued unconditionally
+// (past the end they re-read the last item, unused), so no branch separates
+// them from the compute and the compiler waits for the older loads alone.
 template <int NW, typename Buf, typename Item, typename Load, typename Compute>
 __device__ __forceinline__ void stream_items(int w, int n_items, Item item, Load load, Compute compute) {
+  if (w >= n_items) return;
   Buf A, B;
-  int alo = 0, ahi = 0, blo = 0, bhi = 0;
-  uint32_t ahm = 0, bhm = 0;
+  int alo, ahi, blo, bhi;
+  uint32_t ahm, bhm;
   int j = w;
-  if (j < n_items) {
-    item(j, alo, ahi, ahm);
-    load(alo, ahi, A);
-  }
-  while (j < n_items) {
-    const int j2 = j + NW;
-    if (j2 < n_items) {
-      item(j2, blo, bhi, bhm);
-      load(blo, bhi, B);
-    }
+  item(j, alo, ahi, ahm);
+  load(alo, ahi, A);
+  item(min(j + NW, n_items - 1), blo, bhi, bhm);
+  load(blo, bhi, B);
+  if (w + 3 * NW >= n_items) {
+    // at most three items for this wave (the common sparse case): straight-line
+    // code, every tile's loads issued before the first wait
+    Buf C;
+    int clo, chi;
+    uint32_t chm;
+    item(min(j + 2 * NW, n_items - 1), clo, chi, chm);
+    load(clo, chi, C);
+    __builtin_amdgcn_sched_barrier(0);
     compute(alo, ahi, ahm, A);
-    if (j2 >= n_items) break;
-    const int j3 = j2 + NW;
-    if (j3 < n_items) {
-      item(j3, alo, ahi, ahm);
-      load(alo, ahi, A);
-    }
+    if (w + NW < n_items) compute(blo, bhi, bhm, B);
+    if (w + 2 * NW < n_items) compute(clo, chi, chm, C);
+    return;
+  }
+  for (;;) {
+    __builtin_amdgcn_sched_barrier(0);
+    compute(alo, ahi, ahm, A);
+    j += NW;
+    if (j >= n_items) break;
+    item(min(j + NW, n_items - 1), alo, ahi, ahm);
+    load(alo, ahi, A);
+    __builtin_amdgcn_sched_barrier(0);
     compute(blo, bhi, bhm, B);
-    j = j3;
+    j += NW;
+    if (j >= n_items) break;
+    item(min(j + NW, n_items - 1), blo, bhi, bhm);
+    load(blo, bhi, B);
   }
 }
 
@@ -301,17 +370,19 @@ __global__ __launch_bounds__(NT) void decode_kernel(DecodeArgs a) {
   __shared__ int s_cnt[GMAX];
   __shared__ int s_misc[NW + 2];
 
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // groups fastest in the grid: consecutive workgroups land on different XCDs
+  const Grp gr = group_of(a, blockIdx.x);
+  const int split = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int seg = lane % LPR, rsub = lane / LPR;
-  const int G = a.G;
+  const int G = gr.G;
   const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
   const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
 
-  stage_q<NT, GMAX, D>(s_q, a.q, a.qdt, (int64_t)b * a.qsb + (int64_t)kvh * G * a.qsh, a.qsh, G, a.scale_log2);
-  const Slice sl = build_slice<NT>(a, b, kvh, split, nb, s_dyn_raw, s_cnt, s_misc);
+  stage_q<NT, GMAX, D>(s_q, a.q, a.qdt, (int64_t)b * a.qsb + (int64_t)gr.h0 * a.qsh, a.qsh, G, a.scale_log2);
+  const Slice sl = build_slice<NT>(a, b, gr, split, nb, s_dyn_raw, s_cnt, s_misc);
   if (sl.U == 0) {
-    if (split == 0) write_nan_outputs(a, b, kvh, D, NT);
+    if (split == 0) write_nan_outputs(a, b, gr, D, NT);
     return;
   }
   if (sl.lo >= sl.hi) return;
@@ -339,7 +410,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int e = 0; e < EPV; ++e) acc[g][e] = 0.f;
   }
-  const int64_t head_off = ((int64_t)b * a.sb + (int64_t)kvh * a.sh + seg * EPV) * EB;
+  const int64_t head_off = ((int64_t)b * a.sb + (int64_t)gr.kv * a.sh + seg * EPV) * EB;
   const char* kbase = reinterpret_cast<const char*>(a.k) + head_off;
   const char* vbase = reinterpret_cast<const char*>(a.v) + head_off;
   const int64_t row_bytes = a.ss * EB;
@@ -350,7 +421,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(DecodeArgs a) {
   // item j: sub-tile (j % n_sub) of list entry (j / n_sub)
   auto item = [&](int j, int& t_lo, int& t_hi, uint32_t& hm) {
     int blk;
-    list_entry(a, s_list, sl.lo, j / n_sub, blk, hm);
+    list_entry(a, gr, s_list, sl.lo, j / n_sub, blk, hm);
     t_lo = blk * a.bs + (j % n_sub) * TT;
     t_hi = min(min(blk * a.bs + a.bs, len), t_lo + TT);
   };
@@ -470,7 +541,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(DecodeArgs a) {
       }
     }
   }
-  finish<NT, D, GMAX, HC>(a, b, kvh, split, sl, s_m, s_l, s_acc, s_misc, [&](int g0, int n) {
+  finish<NT, D, GMAX, HC>(a, b, gr, split, sl, s_m, s_l, s_acc, s_misc, [&](int g0, int n) {
     if (rsub == 0) {
 #pragma unroll
       for (int gg = 0; gg < HC; ++gg)
@@ -531,10 +602,12 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeArgs a) {
   __shared__ int s_cnt[GMAX];
   __shared__ int s_misc[NW + 2];
 
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // groups fastest in the grid: consecutive workgroups land on different XCDs
+  const Grp gr = group_of(a, blockIdx.x);
+  const int split = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int col = lane & 15, grp = lane >> 4;     // MFMA lane coordinates
-  const int G = a.G;
+  const int G = gr.G;
   const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
   const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
 
@@ -543,7 +616,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeArgs a) {
   uint4 qf[KS];
   with_dtype(a.qdt, [&](auto tag) {
     constexpr int QDT = decltype(tag)::value;
-    const int64_t qo = (int64_t)b * a.qsb + (int64_t)(kvh * G + min(col, G - 1)) * a.qsh + (D / 4) * grp;
+    const int64_t qo = (int64_t)b * a.qsb + (int64_t)(gr.h0 + min(col, G - 1)) * a.qsh + (D / 4) * grp;
     float x[KS][8];
 #pragma unroll
     for (int s = 0; s < KS; ++s)
@@ -557,16 +630,16 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeArgs a) {
       qf[s] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
     }
   });
-  const Slice sl = build_slice<NT>(a, b, kvh, split, nb, s_dyn_raw, s_cnt, s_misc);
+  const Slice sl = build_slice<NT>(a, b, gr, split, nb, s_dyn_raw, s_cnt, s_misc);
   if (sl.U == 0) {
-    if (split == 0) write_nan_outputs(a, b, kvh, D, NT);
+    if (split == 0) write_nan_outputs(a, b, gr, D, NT);
     return;
   }
   if (sl.lo >= sl.hi) return;
   const uint32_t* s_list = list_base(a, s_dyn_raw);
 
   // lane (col, grp) loads token col of a 16-token tile, elements [D/4*grp, D/4*(grp+1)) of its row
-  const int64_t head_off = ((int64_t)b * a.sb + (int64_t)kvh * a.sh + (D / 4) * grp) * 2;
+  const int64_t head_off = ((int64_t)b * a.sb + (int64_t)gr.kv * a.sh + (D / 4) * grp) * 2;
   const char* kbase = reinterpret_cast<const char*>(a.k) + head_off;
   const char* vbase = reinterpret_cast<const char*>(a.v) + head_off;
   const int64_t row_bytes = a.ss * 2;
@@ -584,7 +657,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeArgs a) {
   struct Buf { uint4 k[KS], v[KS]; };
   auto item = [&](int j, int& t0, int& t_hi, uint32_t& hm) {
     int blk;
-    list_entry(a, s_list, sl.lo, j / n_sub, blk, hm);
+    list_entry(a, gr, s_list, sl.lo, j / n_sub, blk, hm);
     t0 = blk * a.bs + (j % n_sub) * 16;
     t_hi = min(min(blk * a.bs + a.bs, len), t0 + 16);
   };
@@ -671,7 +744,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeArgs a) {
   }
   __syncthreads();                                  // the V tiles are dead: s_big becomes s_acc
   auto s_acc = reinterpret_cast<float (*)[HC][D]>(s_big);
-  finish<NT, D, GMAX, HC>(a, b, kvh, split, sl, s_m, s_l, s_acc, s_misc, [&](int g0, int n) {
+  finish<NT, D, GMAX, HC>(a, b, gr, split, sl, s_m, s_l, s_acc, s_misc, [&](int g0, int n) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int head = 4 * grp + i;
@@ -730,7 +803,8 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
 
 template <int KVDT, int D, int NT, bool MFMA>
 hipError_t launch_g(const DecodeArgs& a, size_t dyn, hipStream_t s) {
-  dim3 grid(a.nsplit, a.Hkv, a.B);
+  dim3 grid(a.per_head ? a.Hq : a.Hkv, a.nsplit, a.B);
+  const int ge = a.per_head ? 1 : a.G;
 #define ADAKV_LAUNCH(GM)                                                                          \
   do {                                                                                            \
     if constexpr (MFMA)                                                                           \
@@ -738,9 +812,9 @@ hipError_t launch_g(const DecodeArgs& a, size_t dyn, hipStream_t s) {
     else                                                                                          \
       hipLaunchKernelGGL((decode_kernel<KVDT, D, GM, NT>), grid, dim3(NT), dyn, s, a);            \
   } while (0)
-  if (a.G <= 1) ADAKV_LAUNCH(1);
-  else if (a.G <= 2) ADAKV_LAUNCH(2);
-  else if (a.G <= 4) ADAKV_LAUNCH(4);
+  if (ge <= 1) ADAKV_LAUNCH(1);
+  else if (ge <= 2) ADAKV_LAUNCH(2);
+  else if (ge <= 4) ADAKV_LAUNCH(4);
   else ADAKV_LAUNCH(8);
 #undef ADAKV_LAUNCH
   return hipGetLastError();
@@ -750,7 +824,7 @@ template <int KVDT, int D>
 hipError_t launch_d(const DecodeArgs& a, hipStream_t s) {
   constexpr bool kMfma = KVDT != ADAKV_F32;
   if (a.table) {
-    const size_t dyn = ((size_t)a.Hq * 8 + 15) / 16 * 16 + (size_t)(((a.max_blocks + 3) / 4) + a.list_cap) * 4;
+    const size_t dyn = ((size_t)a.Hq * 8 + 15) / 16 * 16 + (size_t)(((a.max_blocks + 3) / 4 + 3) / 4 * 4 + a.list_cap) * 4;
     // head_dim 256 in matrix-core mode: 4 waves keep the V tiles within 64 KiB
     constexpr int NT = (kMfma && D >= 256) ? 256 : kSparseThreads;
     return launch_g<KVDT, D, NT, kMfma>(a, dyn, s);

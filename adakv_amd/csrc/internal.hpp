@@ -101,6 +101,8 @@ struct DecodeArgs {
   int max_blocks;
   int list_cap;                // entries of the per-workgroup block list in LDS
   int merge_in_kernel;         // 1: last split merges (sparse); 0: a merge kernel follows (dense)
+  int per_head;                // 1: one workgroup group per q-head (sparse), 0: per KV head
+  int table_unique;            // 1: the first sel_lens entries of a row are distinct valid blocks
 };
 
 struct MergeArgs {

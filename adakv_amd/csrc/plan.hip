@@ -354,11 +354,11 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
   constexpr int NW = NT / kWave;
   using Mask = MaskT<IPT>;
   constexpr Mask kOne = 1;
-  __shared__ uint64_t s_keys[kSortCap];
+  __shared__ __align__(16) uint64_t s_keys[kSortCap];
   __shared__ int s_hist[256];
   __shared__ float s_r[NW][5];
   __shared__ int s_rank[kSortCap];
-  __shared__ float s_max[NT];             // chunk content maxima (+ appended rows)
+  __shared__ __align__(16) float s_max[NT];   // chunk content maxima (+ appended rows)
   __shared__ float s_tau;
   __shared__ int s_mrank[NT];
   __shared__ float s_f[NW];
@@ -436,6 +436,7 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
     }
   }
   const int n_max = min(n_chunks + (nb - rows_in_chunks), NT);
+  if (tid >= n_max && tid < ((n_max + 3) & ~3)) s_max[tid] = -INFINITY;
   if (__ballot(has) != 0) {                    // waves without partials skip the reductions
     const float M = wave_allreduce(pt.m, OpMax());
     float S = 0.f, T = 0.f;
@@ -459,15 +460,19 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
   // top KC is; missing maxima only lower tau.  Ranks of the maxima are
   // counted with the pairs spread over the workgroup.
   if (n_max >= KC) {
+    const int n4 = (n_max + 3) & ~3;           // padded with -inf: never ranks above anything
     const int npad = next_pow2(max(n_max, 1));
-    const int parts = max(NT / npad, 1), jlen = ceil_div(n_max, parts);
-    const int i = tid % npad, j0 = (tid / npad) * jlen, j1 = min(n_max, j0 + jlen);
+    const int parts = max(NT / npad, 1), jlen = (ceil_div(n4, parts) + 3) & ~3;
+    const int i = tid % npad, j0 = (tid / npad) * jlen, j1 = min(n4, j0 + jlen);
     if (i < n_max && tid / npad < parts) {
       const float x = s_max[i];
       int r = 0;
-      for (int j = j0; j < j1; ++j) {
-        const float y = s_max[j];
-        r += (y > x) || (y == x && j < i);
+      for (int j = j0; j < j1; j += 4) {
+        const float4 y = *reinterpret_cast<const float4*>(&s_max[j]);
+        r += (y.x > x) || (y.x == x && j < i);
+        r += (y.y > x) || (y.y == x && j + 1 < i);
+        r += (y.z > x) || (y.z == x && j + 2 < i);
+        r += (y.w > x) || (y.w == x && j + 3 < i);
       }
       if (r) atomicAdd(&s_mrank[i], r);
     }
@@ -477,32 +482,47 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
   }
   __syncthreads();
 
-  // ---- candidates: content scores >= tau, compacted wave by wave ----
+  // ---- candidates: content scores >= tau, one LDS atomic per wave ----
   const float tau = s_tau;
   const bool exact_low = tau == -FLT_MAX;      // compare sanitised scores only at the bottom of the range
+  Mask cm = 0;
 #pragma unroll
-  for (int i = 0; i < IPT; ++i) {
-    const bool c = ((content >> i) & kOne) && (exact_low ? sanitize(v[i]) >= tau : v[i] >= tau);
-    const uint64_t bal = __ballot(c);
-    if (bal) {
+  for (int i = 0; i < IPT; ++i)
+    if (((content >> i) & kOne) && (exact_low ? sanitize(v[i]) >= tau : v[i] >= tau)) cm |= kOne << i;
+  {
+    const int c = popcnt(cm);
+    const int inc = wave_incl_scan(c);
+    const int wtot = __builtin_amdgcn_readlane(inc, kWave - 1);
+    if (wtot) {
       int o0 = 0;
-      if (lane == 0) o0 = atomicAdd(&s_n, __popcll(bal));
-      o0 = __shfl(o0, 0);
-      const int o = o0 + __popcll(bal & ((1ull << lane) - 1ull));
-      if (c && o < kSortCap) s_keys[o] = sel_key(sanitize(v[i]), base + i);
+      if (lane == kWave - 1) o0 = atomicAdd(&s_n, wtot);
+      int o = __builtin_amdgcn_readlane(o0, kWave - 1) + inc - c;
+#pragma unroll
+      for (int i = 0; i < IPT; ++i) {
+        if ((cm >> i) & kOne) {
+          if (o < kSortCap) s_keys[o] = sel_key(sanitize(v[i]), base + i);
+          ++o;
+        }
+      }
     }
   }
   __syncthreads();
   const int n_cand = s_n;
   if (n_cand <= kSortCap) {
     // rank every candidate against all others, the pairs spread over the workgroup
+    if (tid == 0 && (n_cand & 1)) s_keys[n_cand] = 0;   // pad to pairs: key 0 ranks below every key
+    __syncthreads();
+    const int n2 = (n_cand + 1) & ~1;
     const int npad = next_pow2(max(n_cand, 1));
-    const int parts = max(NT / npad, 1), jlen = ceil_div(n_cand, parts);
-    const int i = tid % npad, j0 = (tid / npad) * jlen, j1 = min(n_cand, j0 + jlen);
+    const int parts = max(NT / npad, 1), jlen = (ceil_div(n2, parts) + 1) & ~1;
+    const int i = tid % npad, j0 = (tid / npad) * jlen, j1 = min(n2, j0 + jlen);
     if (i < n_cand && tid / npad < parts) {
       const uint64_t ki = s_keys[i];
       int r = 0;
-      for (int j = j0; j < j1; ++j) r += s_keys[j] > ki;
+      for (int j = j0; j < j1; j += 2) {
+        const ulonglong2 y = *reinterpret_cast<const ulonglong2*>(&s_keys[j]);
+        r += (y.x > ki) + (y.y > ki);
+      }
       if (r) atomicAdd(&s_rank[i], r);
     }
     __syncthreads();
