@@ -45,6 +45,25 @@ __device__ __forceinline__ float sanitize(float x) {
   return fminf(fmaxf(x, -FLT_MAX), FLT_MAX);
 }
 
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+template <int DT>
+__device__ __forceinline__ float4_t mfma_16x16x32(const uint4& a, const uint4& b, float4_t c) {
+  if constexpr (DT == ADAKV_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+}
+template <int DT>
+__device__ __forceinline__ uint32_t pack2_typed(float lo, float hi) {
+  if constexpr (DT == ADAKV_BF16) return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  else return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+}
+
 // ---------------------------------------------------------------- scores ----
 // Decode-time append (adakv/estimator.py:62-74): block r gained tokens, so its
 // centroid becomes the sequential fp32 mean of its real tokens (summed in
@@ -102,15 +121,21 @@ __device__ void append_block(const ScoreArgs& a, int b, int kvh, int r, int len,
   }
 }
 
-// Scores of every block of every (sequence, KV head) against its G q-heads.
-// 1-D grid: first n_app workgroups per (sequence, KV head) for the appended
-// blocks (dispatched first: their dependent K loads are the longest chain),
-// then n_chunks workgroups per (sequence, KV head) of CB blocks each.  A chunk
-// workgroup stages the G queries through LDS into registers and reads every
-// centroid row once with 16-byte loads, dotting it with all G queries (fp32
-// FMA, then a DPP butterfly over the lanes sharing the row).
+// Softmax partial of a chunk for one head, written by one lane: see the
+// PartRecord layout in internal.hpp.
+__device__ __forceinline__ void write_part(const ScoreArgs& a, int b, int h, int chunk, float m, float S, float T,
+                                           float lo, float hi) {
+  float4* rec = reinterpret_cast<float4*>(a.parts + (((int64_t)b * a.Hq + h) * a.parts_pitch + chunk) * kPartFloats);
+  rec[0] = make_float4(m, S, T, lo);
+  rec[1] = make_float4(hi, 0.f, 0.f, 0.f);
+}
+
+// fp32 centroids: one workgroup per chunk of CB blocks; every centroid row is
+// read once with 16-byte loads and dotted with the G queries (fp32 FMA, then a
+// DPP butterfly over the lanes sharing the row); one partial per chunk.
 template <int CDT, int D, int GMAX>
-__global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
+__device__ void score_chunk_valu(const ScoreArgs& a, int b, int kvh, int unit, int nb, int nrows,
+                                 float (*s_q)[D], float* s_sc_flat) {
   constexpr int EPV = Elt<CDT>::kPerVec;
   constexpr int EB = Elt<CDT>::kBytes;
   constexpr int LPR = D / EPV;              // lanes per centroid row
@@ -118,41 +143,10 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
   constexpr int NLD = 4;                    // loads in flight per lane
   constexpr int RPW = RPL * NLD;            // rows per wave
   constexpr int CB = (kNT / kWave) * RPW;   // rows (blocks) per workgroup
-  __shared__ float s_q[GMAX][D];
-  __shared__ float s_sc[GMAX][CB];
-  __shared__ float s_tile[kNT * 8];
-  __shared__ float s_red[GMAX][kNT / kWave];
-
-  int id = blockIdx.x;
-  const bool app = id < a.n_app * a.Hkv * a.B;
-  int unit, kvh, b;
-  if (app) {
-    unit = id % a.n_app; id /= a.n_app;
-  } else {
-    id -= a.n_app * a.Hkv * a.B;
-    unit = id % a.n_chunks; id /= a.n_chunks;
-  }
-  kvh = id % a.Hkv;
-  b = id / a.Hkv;
-  const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
-  const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
-  const int first_app = a.n_new > 0 ? max(len - a.n_new, 0) / a.bs : nb;
+  auto s_sc = reinterpret_cast<float (*)[CB]>(s_sc_flat);
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int G = a.G;
-  const int64_t qbase = (int64_t)b * a.qsb + (int64_t)kvh * G * a.qsh;
-
-  if (app) {
-    const int r = first_app + unit;
-    if (r >= nb) return;
-    stage_q<kNT, GMAX, D>(s_q, a.q, a.qdt, qbase, a.qsh, G, 1.f);
-    with_dtype(a.kdt, [&](auto tag) {
-      append_block<CDT, decltype(tag)::value, D, GMAX>(a, b, kvh, r, len, s_q, s_tile, s_red);
-    });
-    return;
-  }
   const int row0 = unit * CB;
-  const int nrows = min(nb, first_app);     // appended blocks are scored by their own workgroups
-  if (row0 >= nrows) return;
   const int seg = lane % LPR, rsub = lane / LPR;
   const int64_t cbase_el = (((int64_t)b * a.Hkv + kvh) * a.max_blocks) * D;
   const char* cbase = reinterpret_cast<const char*>(a.c) + cbase_el * EB;
@@ -162,7 +156,7 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
     const int r = min(row0 + w * RPW + i * RPL + rsub, nrows - 1);   // in bounds; extra rows unused
     cv[i] = load16(cbase + ((int64_t)r * D + seg * EPV) * EB);
   }
-  stage_q<kNT, GMAX, D>(s_q, a.q, a.qdt, qbase, a.qsh, G, 1.f);
+  stage_q<kNT, GMAX, D>(s_q, a.q, a.qdt, (int64_t)b * a.qsb + (int64_t)kvh * G * a.qsh, a.qsh, G, 1.f);
   __syncthreads();
   float qv[GMAX][EPV];
 #pragma unroll
@@ -229,12 +223,169 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
     T = wave_allreduce(T, OpAdd());
     lo = wave_allreduce(lo, OpMin());
     hi = wave_allreduce(hi, OpMax());
-    if (lane == 0) {
-      float4* rec = reinterpret_cast<float4*>(a.parts + (((int64_t)b * a.Hq + kvh * G + g) * a.parts_pitch + unit) *
-                                                            kPartFloats);
-      rec[0] = make_float4(m, S, T, lo);
-      rec[1] = make_float4(hi, 0.f, 0.f, 0.f);
+    if (lane == 0) write_part(a, b, kvh * G + g, unit, m, S, T, lo, hi);
+  }
+}
+
+// bf16 / fp16 centroids on the matrix cores: S = C . Q^T with
+// v_mfma_f32_16x16x32 -- a wave holds 4 tiles of 16 centroid rows in the
+// A-operand layout (lane l: row l%16, a contiguous D/2-byte slice of it, all
+// loads issued at once), the group's q-heads, zero-padded to 16, form the B
+// operand.  Result lane (col, grp) holds the scores of rows 4*grp .. +3 of a
+// tile for head col: written as 16-byte stores, and reduced over the wave's
+// 64 rows into that head's softmax partial (one partial per wave).
+template <int CDT, int D, int GMAX>
+__device__ void score_chunk_mfma(const ScoreArgs& a, int b, int kvh, int unit, int nb, int nrows) {
+  static_assert(D % 32 == 0 && GMAX <= 16, "16x16 tiles over head_dim");
+  constexpr int KS = D / 32;                // k-steps (16-byte loads per lane per tile)
+  constexpr int TPW = 4;                    // tiles per wave
+  constexpr int RPW = 16 * TPW;             // rows per wave = rows per partial
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  const int col = lane & 15, grp = lane >> 4;
+  const int G = a.G;
+  const int wrow0 = unit * (kNT / kWave) * RPW + w * RPW;
+  if (wrow0 >= nrows) return;
+  // A fragments: lane (col, grp) reads row wrow0 + 16t + col, elements [D/4*grp, D/4*(grp+1))
+  const char* cbase = reinterpret_cast<const char*>(a.c) +
+                      ((((int64_t)b * a.Hkv + kvh) * a.max_blocks) * D + (D / 4) * grp) * 2;
+  uint4 cf[TPW][KS];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int r = min(wrow0 + 16 * t + col, nrows - 1);     // in bounds; extra rows masked below
+#pragma unroll
+    for (int s = 0; s < KS; ++s) cf[t][s] = load16(cbase + (int64_t)r * D * 2 + 16 * s);
+  }
+  // B fragments: lane (col, grp) holds q[head col][D/4*grp + 8s .. +7]
+  uint4 qf[KS];
+  with_dtype(a.qdt, [&](auto tag) {
+    constexpr int QDT = decltype(tag)::value;
+    const int64_t qo = (int64_t)b * a.qsb + (int64_t)(kvh * G + min(col, G - 1)) * a.qsh + (D / 4) * grp;
+    float x[KS][8];
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[s][u] = load_t<QDT>(a.q, qo + 8 * s + u);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      uint32_t wv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) wv[u] = col < G ? pack2_typed<CDT>(x[s][2 * u], x[s][2 * u + 1]) : 0u;
+      qf[s] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
     }
+  });
+  float sc[TPW][4];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) acc = mfma_16x16x32<CDT>(cf[t][s], qf[s], acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[t][i] = acc[i];
+  }
+  // scores: rows 4*grp + i of each tile, head col
+  if (col < G) {
+    float* srow = a.scores + ((int64_t)b * a.Hq + kvh * G + col) * a.sp;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int r = wrow0 + 16 * t + 4 * grp;
+      if (r + 3 < nrows) {
+        *reinterpret_cast<float4*>(srow + r) = make_float4(sc[t][0], sc[t][1], sc[t][2], sc[t][3]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (r + i < nrows) srow[r + i] = sc[t][i];
+      }
+    }
+  }
+  if (a.parts == nullptr) return;
+  // softmax partial of the wave's rows for head col (lanes col, col+16, col+32, col+48)
+  const Bounds bb = budget_bounds(nb, a.cfg);
+  const int c_lo = bb.sink, c_hi = nb - bb.local;
+  const float tf = (float)fmax(a.cfg.temperature, 1e-6);
+  float m = -INFINITY, lo = FLT_MAX, hi = -FLT_MAX;
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = wrow0 + 16 * t + 4 * grp + i;
+      const float x = sc[t][i];
+      const bool ok = r < nrows;
+      sc[t][i] = ok ? (tf == 1.f ? x : __fdiv_rn(x, tf)) : -INFINITY;
+      m = fmaxf(m, sc[t][i]);
+      if (ok && r >= c_lo && r < c_hi) {
+        const float xs = sanitize(x);
+        lo = fminf(lo, xs);
+        hi = fmaxf(hi, xs);
+      }
+    }
+  }
+  LanePair pr = swap16(m);
+  m = fmaxf(pr.a, pr.b);
+  pr = swap32(m);
+  m = fmaxf(pr.a, pr.b);
+  float S = 0.f, T = 0.f;
+  if (m != -INFINITY) {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (sc[t][i] != -INFINITY) {
+          const float e = __expf(sc[t][i] - m);
+          S += e;
+          T = fmaf(e, sc[t][i] - m, T);
+        }
+  }
+  pr = swap16(S); S = pr.a + pr.b; pr = swap32(S); S = pr.a + pr.b;
+  pr = swap16(T); T = pr.a + pr.b; pr = swap32(T); T = pr.a + pr.b;
+  pr = swap16(lo); lo = fminf(pr.a, pr.b); pr = swap32(lo); lo = fminf(pr.a, pr.b);
+  pr = swap16(hi); hi = fmaxf(pr.a, pr.b); pr = swap32(hi); hi = fmaxf(pr.a, pr.b);
+  if (grp == 0 && col < G) write_part(a, b, kvh * G + col, wrow0 / RPW, m, S, T, lo, hi);
+}
+
+// Scores of every block of every (sequence, KV head) against its G q-heads.
+// 1-D grid: first n_app workgroups per (sequence, KV head) for the appended
+// blocks (dispatched first: their dependent K loads are the longest chain),
+// then n_chunks workgroups per (sequence, KV head).
+template <int CDT, int D, int GMAX>
+__global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
+  constexpr bool kMfma = CDT != ADAKV_F32;
+  constexpr int CBV = (kNT / kWave) * (kWave / (D / Elt<CDT>::kPerVec)) * 4;   // VALU rows per workgroup
+  __shared__ float s_q[GMAX][D];
+  __shared__ float s_sc[kMfma ? 1 : GMAX * CBV];
+  __shared__ float s_tile[kNT * 8];
+  __shared__ float s_red[GMAX][kNT / kWave];
+
+  int id = blockIdx.x;
+  const bool app = id < a.n_app * a.Hkv * a.B;
+  int unit, kvh, b;
+  if (app) {
+    unit = id % a.n_app; id /= a.n_app;
+  } else {
+    id -= a.n_app * a.Hkv * a.B;
+    unit = id % a.n_chunks; id /= a.n_chunks;
+  }
+  kvh = id % a.Hkv;
+  b = id / a.Hkv;
+  const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
+  const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
+  const int first_app = a.n_new > 0 ? max(len - a.n_new, 0) / a.bs : nb;
+  const int G = a.G;
+
+  if (app) {
+    const int r = first_app + unit;
+    if (r >= nb) return;
+    stage_q<kNT, GMAX, D>(s_q, a.q, a.qdt, (int64_t)b * a.qsb + (int64_t)kvh * G * a.qsh, a.qsh, G, 1.f);
+    with_dtype(a.kdt, [&](auto tag) {
+      append_block<CDT, decltype(tag)::value, D, GMAX>(a, b, kvh, r, len, s_q, s_tile, s_red);
+    });
+    return;
+  }
+  const int nrows = min(nb, first_app);     // appended blocks are scored by their own workgroups
+  if constexpr (kMfma) {
+    score_chunk_mfma<CDT, D, GMAX>(a, b, kvh, unit, nb, nrows);
+  } else {
+    if (unit * CBV >= nrows) return;
+    score_chunk_valu<CDT, D, GMAX>(a, b, kvh, unit, nb, nrows, s_q, s_sc);
   }
 }
 
@@ -660,10 +811,14 @@ __global__ __launch_bounds__(kNT) void budget_kernel(BudgetArgs a) {
 
 template <int CDT, int D>
 hipError_t launch_score_d(ScoreArgs& a, hipStream_t s) {
-  constexpr int EPV = Elt<CDT>::kPerVec;
-  constexpr int CB = (kNT / kWave) * (kWave / (D / EPV)) * 4;
-  a.chunk_rows = CB;
-  a.n_chunks = (a.max_blocks + CB - 1) / CB;
+  if constexpr (CDT == ADAKV_F32) {
+    constexpr int CB = (kNT / kWave) * (kWave / (D / 4)) * 4;   // rows per workgroup = rows per partial
+    a.chunk_rows = CB;
+    a.n_chunks = (a.max_blocks + CB - 1) / CB;
+  } else {
+    a.chunk_rows = 64;                                          // rows per wave = rows per partial
+    a.n_chunks = (a.max_blocks + 4 * 64 - 1) / (4 * 64);        // 4 waves per workgroup
+  }
   // blocks holding the newest n_new tokens: at most ceil(n_new / bs) + 1
   a.n_app = a.n_new > 0 ? std::min((a.n_new + a.bs - 1) / a.bs + 1, a.max_blocks) : 0;
   dim3 grid((unsigned)((int64_t)(a.n_app + a.n_chunks) * a.Hkv * a.B));
