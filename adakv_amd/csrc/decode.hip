@@ -300,38 +300,54 @@ __device__ void finish(const DecodeArgs& a, int b, const Grp& gr, int split, con
   if (tid == 0) reset_counter(&a.counters[(int64_t)b * gr.ng + gr.unit]);
 }
 
-// Streams items j = w, w + NW, ... of a slice with two items in flight: the
-// next item's loads are outstanding while the current one is computed, and a
-// buffer is refilled right after its compute.  item(j, t_lo, t_hi, hm)
+// Streams items j = w, w + NW, ... of a slice.  item(j, t_lo, t_hi, hm)
 // describes item j, load(t_lo, t_hi, buf) issues its loads, compute(t_lo,
-// t_hi, hm, buf) consumes them.  Look-ahead loads are issued unconditionally
-// (past the end they re-read the last item, unused), so no branch separates
-// them from the compute and the compiler waits for the older loads alone.
+// t_hi, hm, buf) consumes them.  Up to three items per wave are loaded at
+// once; beyond that two items are in flight (the next item's loads are
+// outstanding while the current one is computed, and a buffer is refilled
+// right after its compute; past the end a look-ahead re-reads the last item).
 template <int NW, typename Buf, typename Item, typename Load, typename Compute>
 __device__ __forceinline__ void stream_items(int w, int n_items, Item item, Load load, Compute compute) {
   if (w >= n_items) return;
+  const int mine = (n_items - w + NW - 1) / NW;    // items of this wave (wave-uniform)
   Buf A, B;
   int alo, ahi, blo, bhi;
   uint32_t ahm, bhm;
   int j = w;
-  item(j, alo, ahi, ahm);
-  load(alo, ahi, A);
-  item(min(j + NW, n_items - 1), blo, bhi, bhm);
-  load(blo, bhi, B);
-  if (w + 3 * NW >= n_items) {
-    // at most three items for this wave (the common sparse case): straight-line
-    // code, every tile's loads issued before the first wait
+  if (mine <= 3) {
+    // the common sparse case: straight-line code per count, every tile's
+    // loads issued before the first wait and no load issued for nothing
+    // (a wave's loads share the CU's vector-memory pipeline with the others)
+    item(j, alo, ahi, ahm);
+    load(alo, ahi, A);
+    if (mine == 1) {
+      __builtin_amdgcn_sched_barrier(0);
+      compute(alo, ahi, ahm, A);
+      return;
+    }
+    item(j + NW, blo, bhi, bhm);
+    load(blo, bhi, B);
+    if (mine == 2) {
+      __builtin_amdgcn_sched_barrier(0);
+      compute(alo, ahi, ahm, A);
+      compute(blo, bhi, bhm, B);
+      return;
+    }
     Buf C;
     int clo, chi;
     uint32_t chm;
-    item(min(j + 2 * NW, n_items - 1), clo, chi, chm);
+    item(j + 2 * NW, clo, chi, chm);
     load(clo, chi, C);
     __builtin_amdgcn_sched_barrier(0);
     compute(alo, ahi, ahm, A);
-    if (w + NW < n_items) compute(blo, bhi, bhm, B);
-    if (w + 2 * NW < n_items) compute(clo, chi, chm, C);
+    compute(blo, bhi, bhm, B);
+    compute(clo, chi, chm, C);
     return;
   }
+  item(j, alo, ahi, ahm);
+  load(alo, ahi, A);
+  item(j + NW, blo, bhi, bhm);
+  load(blo, bhi, B);
   for (;;) {
     __builtin_amdgcn_sched_barrier(0);
     compute(alo, ahi, ahm, A);
