@@ -69,55 +69,49 @@ __device__ __forceinline__ uint32_t pack2_typed(float lo, float hi) {
 // centroid becomes the sequential fp32 mean of its real tokens (summed in
 // token order, one correctly rounded division, one rounding to the centroid
 // type); the new centroid is stored and scored against the G q-heads.  One
-// workgroup per appended block: each pass loads up to kNT / (D / 8) token rows
-// at once with 16-byte loads, stages them through LDS and adds them column by
-// column in token order.
+// workgroup per appended block; thread d owns column d: it loads that column
+// of up to 16 token rows at once (every load instruction covers one row,
+// coalesced) and adds them in token order in registers.
 template <int CDT, int KDT, int D, int GMAX>
-__device__ void append_block(const ScoreArgs& a, int b, int kvh, int r, int len, const float (*s_q)[D],
-                             float* s_tile, float (*s_red)[kNT / kWave]) {
-  constexpr int EPV = Elt<KDT>::kPerVec;
-  constexpr int EB = Elt<KDT>::kBytes;
-  constexpr int LPR = D / EPV;                 // lanes per token row
-  constexpr int RP = kNT / LPR;                // token rows per pass
+__device__ void append_block(const ScoreArgs& a, int b, int kvh, int r, int len, float (*s_red)[kNT / kWave]) {
+  constexpr int TB = 16;                       // token rows loaded together
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
-  const int row = tid / LPR, seg = tid % LPR;
+  const int d = min(tid, D - 1);               // threads past D mirror the last column (unused)
   const int t0 = r * a.bs, t1 = min(t0 + a.bs, len);
-  const char* kp = reinterpret_cast<const char*>(a.k) +
-                   ((int64_t)b * a.ksb + (int64_t)kvh * a.ksh + seg * EPV) * EB;
-  float acc = 0.f;
-  for (int p0 = t0; p0 < t1; p0 += RP) {
-    const int t = min(p0 + row, t1 - 1);       // in bounds; rows past t1 are not summed
-    float x[EPV];
-    unpack<KDT>(load16(kp + (int64_t)t * a.kss * EB), x);
-    __syncthreads();                           // the previous pass's tile has been consumed
+  const int G = a.G;
+  // the query column first: its loads overlap the key loads
+  float qd[GMAX];
+  with_dtype(a.qdt, [&](auto tag) {
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) s_tile[row * D + seg * EPV + e] = x[e];
-    __syncthreads();
-    if (tid < D) {
-      const int n = min(RP, t1 - p0);
-      for (int j = 0; j < n; ++j) acc = (p0 + j == t0) ? s_tile[j * D + tid] : acc + s_tile[j * D + tid];
-    }
+    for (int g = 0; g < GMAX; ++g)
+      qd[g] = load_t<decltype(tag)::value>(a.q, (int64_t)b * a.qsb + (int64_t)(kvh * G + min(g, G - 1)) * a.qsh + d);
+  });
+  const int64_t kcol = (int64_t)b * a.ksb + (int64_t)kvh * a.ksh + d;
+  float acc = 0.f;
+  for (int p0 = t0; p0 < t1; p0 += TB) {
+    float x[TB];
+#pragma unroll
+    for (int j = 0; j < TB; ++j) x[j] = load_t<KDT>(a.k, kcol + (int64_t)min(p0 + j, t1 - 1) * a.kss);
+#pragma unroll
+    for (int j = 0; j < TB; ++j)
+      if (p0 + j < t1) acc = (p0 + j == t0) ? x[j] : acc + x[j];
   }
-  float c = 0.f;
-  if (tid < D) {
-    const float m = __fdiv_rn(acc, (float)(t1 - t0));
-    store_elt(a.c, CDT, (((int64_t)b * a.Hkv + kvh) * a.max_blocks + r) * D + tid, m);
-    c = round_to(m, CDT);
-  }
+  const float m = __fdiv_rn(acc, (float)(t1 - t0));
+  if (tid < D) store_elt(a.c, CDT, (((int64_t)b * a.Hkv + kvh) * a.max_blocks + r) * D + tid, m);
+  const float c = tid < D ? round_to(m, CDT) : 0.f;
 #pragma unroll
   for (int g = 0; g < GMAX; ++g) {
-    if (g < a.G) {
-      float p = tid < D ? s_q[g][tid] * c : 0.f;
-      p = group_sum<kWave>(p);
+    if (g < G) {
+      const float p = group_sum<kWave>(qd[g] * c);
       if (lane == 0) s_red[g][w] = p;
     }
   }
   __syncthreads();
-  if (tid < a.G) {
+  if (tid < G) {
     float sc = 0.f;
 #pragma unroll
     for (int i = 0; i < kNT / kWave; ++i) sc += s_red[tid][i];
-    a.scores[((int64_t)b * a.Hq + kvh * a.G + tid) * a.sp + r] = sc;
+    a.scores[((int64_t)b * a.Hq + kvh * G + tid) * a.sp + r] = sc;
   }
 }
 
@@ -302,39 +296,47 @@ __device__ void score_chunk_mfma(const ScoreArgs& a, int b, int kvh, int unit, i
   const Bounds bb = budget_bounds(nb, a.cfg);
   const int c_lo = bb.sink, c_hi = nb - bb.local;
   const float tf = (float)fmax(a.cfg.temperature, 1e-6);
+  // branch-free: content and validity are selects, empty rows contribute exp(-inf) = 0
   float m = -INFINITY, lo = FLT_MAX, hi = -FLT_MAX;
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = wrow0 + 16 * t + 4 * grp + i;
-      const float x = sc[t][i];
-      const bool ok = r < nrows;
-      sc[t][i] = ok ? (tf == 1.f ? x : __fdiv_rn(x, tf)) : -INFINITY;
-      m = fmaxf(m, sc[t][i]);
-      if (ok && r >= c_lo && r < c_hi) {
-        const float xs = sanitize(x);
-        lo = fminf(lo, xs);
-        hi = fmaxf(hi, xs);
-      }
+      const bool cont = (r >= c_lo) & (r < c_hi) & (r < nrows);
+      const float xs = sanitize(sc[t][i]);
+      lo = fminf(lo, cont ? xs : FLT_MAX);
+      hi = fmaxf(hi, cont ? xs : -FLT_MAX);
     }
   }
+  if (tf != 1.f) {   // temperature: the correctly rounded division only when it is needed (uniform)
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[t][i] = __fdiv_rn(sc[t][i], tf);
+  }
+#pragma unroll
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sc[t][i] = (wrow0 + 16 * t + 4 * grp + i < nrows) ? sc[t][i] : -INFINITY;
+      m = fmaxf(m, sc[t][i]);
+    }
   LanePair pr = swap16(m);
   m = fmaxf(pr.a, pr.b);
   pr = swap32(m);
   m = fmaxf(pr.a, pr.b);
+  const float mm = m == -INFINITY ? 0.f : m;
   float S = 0.f, T = 0.f;
-  if (m != -INFINITY) {
 #pragma unroll
-    for (int t = 0; t < TPW; ++t)
+  for (int t = 0; t < TPW; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (sc[t][i] != -INFINITY) {
-          const float e = __expf(sc[t][i] - m);
-          S += e;
-          T = fmaf(e, sc[t][i] - m, T);
-        }
-  }
+    for (int i = 0; i < 4; ++i) {
+      const float dz = sc[t][i] - mm;
+      const float e = __expf(dz);
+      S += e;
+      T = fmaf(e, fmaxf(dz, -FLT_MAX), T);
+    }
   pr = swap16(S); S = pr.a + pr.b; pr = swap32(S); S = pr.a + pr.b;
   pr = swap16(T); T = pr.a + pr.b; pr = swap32(T); T = pr.a + pr.b;
   pr = swap16(lo); lo = fminf(pr.a, pr.b); pr = swap32(lo); lo = fminf(pr.a, pr.b);
@@ -352,7 +354,6 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
   constexpr int CBV = (kNT / kWave) * (kWave / (D / Elt<CDT>::kPerVec)) * 4;   // VALU rows per workgroup
   __shared__ float s_q[GMAX][D];
   __shared__ float s_sc[kMfma ? 1 : GMAX * CBV];
-  __shared__ float s_tile[kNT * 8];
   __shared__ float s_red[GMAX][kNT / kWave];
 
   int id = blockIdx.x;
@@ -374,10 +375,7 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
   if (app) {
     const int r = first_app + unit;
     if (r >= nb) return;
-    stage_q<kNT, GMAX, D>(s_q, a.q, a.qdt, (int64_t)b * a.qsb + (int64_t)kvh * G * a.qsh, a.qsh, G, 1.f);
-    with_dtype(a.kdt, [&](auto tag) {
-      append_block<CDT, decltype(tag)::value, D, GMAX>(a, b, kvh, r, len, s_q, s_tile, s_red);
-    });
+    with_dtype(a.kdt, [&](auto tag) { append_block<CDT, decltype(tag)::value, D, GMAX>(a, b, kvh, r, len, s_red); });
     return;
   }
   const int nrows = min(nb, first_app);     // appended blocks are scored by their own workgroups
