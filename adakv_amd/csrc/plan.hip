@@ -497,6 +497,25 @@ __device__ __forceinline__ void write_weight(const SelectArgs& a, int b, int h, 
   }
 }
 
+// One wave: the digit d of a 256-bin histogram (bins indexed by digit, larger
+// digit = larger key) that holds the need-th largest key; out[0] = d, out[1] =
+// keys in larger digits.  out[1] = -1 when the histogram holds fewer than need keys.
+__device__ __forceinline__ void radix_digit(const int* hist, int need, int* out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int c4[4], s4 = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { c4[j] = hist[255 - (4 * lane + j)]; s4 += c4[j]; }
+  const int inc = wave_incl_scan(s4);
+  const int tot = __builtin_amdgcn_readlane(inc, kWave - 1);
+  int before = inc - s4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (before < need && need <= before + c4[j]) { out[0] = 255 - (4 * lane + j); out[1] = before; }
+    before += c4[j];
+  }
+  if (lane == 0 && (tot < need || need <= 0)) { out[0] = 0; out[1] = -1; }
+}
+
 template <int NT, int IPT>
 __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
   static_assert(IPT <= 64 && IPT % 4 == 0 && NT >= 256, "one mask word per thread");
@@ -509,7 +528,7 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
   __shared__ int s_rank[kSortCap];
   __shared__ __align__(16) float s_max[NT];   // chunk content maxima (+ appended rows)
   __shared__ float s_tau;
-  __shared__ int s_mrank[NT];
+  __shared__ int s_rh[512];             // two radix histograms for the threshold
   __shared__ float s_f[NW];
   __shared__ int s_i[NW];
   __shared__ int s_bc[4];
@@ -526,7 +545,7 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
   const bool adaptive = a.cfg.policy == ADAKV_POLICY_ADAPTIVE && nb > 1;
   if (tid == 0) { s_n = 0; s_tau = -FLT_MAX; }
   for (int i = tid; i < kSortCap; i += NT) s_rank[i] = 0;
-  s_mrank[tid] = 0;
+  for (int i = tid; i < 512; i += NT) s_rh[i] = 0;
 
   // ---- forced prefix and padding of the block-table row ----
   int32_t* trow = a.table + ((int64_t)b * a.Hq + h) * a.T;
@@ -604,30 +623,31 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
     return;
   }
 
-  // ---- selection threshold tau: the KC-th largest chunk content maximum ----
-  // At least KC content scores (those maxima) are >= tau, so every one of the
-  // top KC is; missing maxima only lower tau.  Ranks of the maxima are
-  // counted with the pairs spread over the workgroup.
-  if (n_max >= KC) {
-    const int n4 = (n_max + 3) & ~3;           // padded with -inf: never ranks above anything
-    const int npad = next_pow2(max(n_max, 1));
-    const int parts = max(NT / npad, 1), jlen = (ceil_div(n4, parts) + 3) & ~3;
-    const int i = tid % npad, j0 = (tid / npad) * jlen, j1 = min(n4, j0 + jlen);
-    if (i < n_max && tid / npad < parts) {
-      const float x = s_max[i];
-      int r = 0;
-      for (int j = j0; j < j1; j += 4) {
-        const float4 y = *reinterpret_cast<const float4*>(&s_max[j]);
-        r += (y.x > x) || (y.x == x && j < i);
-        r += (y.y > x) || (y.y == x && j + 1 < i);
-        r += (y.z > x) || (y.z == x && j + 2 < i);
-        r += (y.w > x) || (y.w == x && j + 3 < i);
-      }
-      if (r) atomicAdd(&s_mrank[i], r);
-    }
+  // ---- selection threshold tau from the chunk content maxima ----
+  // Two radix passes over the order-preserving keys of the maxima (top byte,
+  // then the next byte within the bin that holds the KC-th largest) give the
+  // 16-bit key prefix of the KC-th largest maximum; tau is the smallest float
+  // with that prefix.  At least KC content scores (those maxima) are >= tau,
+  // so every one of the top KC is; missing maxima only lower tau.
+  {
+    const bool has_max = tid < n_max && s_max[tid] != -INFINITY;
+    const uint32_t key = has_max ? (uint32_t)(sel_key(s_max[tid], 0) >> 32) : 0u;
+    if (has_max) atomicAdd(&s_rh[key >> 24], 1);
     __syncthreads();
-    for (int i2 = tid; i2 < n_max; i2 += NT)
-      if (s_mrank[i2] == KC - 1) s_tau = s_max[i2] == -INFINITY ? -FLT_MAX : s_max[i2];
+    if (w == 0) radix_digit(s_rh, KC, s_bc);          // s_bc[0] = digit, s_bc[1] = count above
+    __syncthreads();
+    const uint32_t b1 = (uint32_t)s_bc[0];
+    const int above1 = s_bc[1];
+    if (has_max && (key >> 24) == b1) atomicAdd(&s_rh[256 + ((key >> 16) & 0xffu)], 1);
+    __syncthreads();
+    if (w == 0) {
+      radix_digit(s_rh + 256, KC - above1, s_bc + 2);
+      if (lane == 0) {
+        const uint32_t tk = (b1 << 24) | ((uint32_t)s_bc[2] << 16);
+        const uint32_t u = (tk & 0x80000000u) ? (tk & 0x7fffffffu) : ~tk;
+        s_tau = (above1 < 0 || s_bc[3] < 0) ? -FLT_MAX : fmaxf(__uint_as_float(u), -FLT_MAX);
+      }
+    }
   }
   __syncthreads();
 
