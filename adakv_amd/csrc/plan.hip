@@ -653,11 +653,15 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
 
   // ---- candidates: content scores >= tau, one LDS atomic per wave ----
   const float tau = s_tau;
-  const bool exact_low = tau == -FLT_MAX;      // compare sanitised scores only at the bottom of the range
   Mask cm = 0;
+  if (tau == -FLT_MAX) {                       // the bottom of the range: compare sanitised scores
 #pragma unroll
-  for (int i = 0; i < IPT; ++i)
-    if (((content >> i) & kOne) && (exact_low ? sanitize(v[i]) >= tau : v[i] >= tau)) cm |= kOne << i;
+    for (int i = 0; i < IPT; ++i) cm |= (sanitize(v[i]) >= tau) ? (kOne << i) : Mask(0);
+  } else {
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) cm |= (v[i] >= tau) ? (kOne << i) : Mask(0);
+  }
+  cm &= content;
   {
     const int c = popcnt(cm);
     const int inc = wave_incl_scan(c);
@@ -668,9 +672,10 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
       int o = __builtin_amdgcn_readlane(o0, kWave - 1) + inc - c;
 #pragma unroll
       for (int i = 0; i < IPT; ++i) {
-        if ((cm >> i) & kOne) {
-          if (o < kSortCap) s_keys[o] = sel_key(sanitize(v[i]), base + i);
-          ++o;
+        const bool bit = (cm >> i) & kOne;
+        if (__ballot(bit)) {                   // most element positions hold no candidate in the wave
+          if (bit && o < kSortCap) s_keys[o] = sel_key(sanitize(v[i]), base + i);
+          o += bit ? 1 : 0;
         }
       }
     }
@@ -688,6 +693,7 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
     if (i < n_cand && tid / npad < parts) {
       const uint64_t ki = s_keys[i];
       int r = 0;
+#pragma unroll 4
       for (int j = j0; j < j1; j += 2) {
         const ulonglong2 y = *reinterpret_cast<const ulonglong2*>(&s_keys[j]);
         r += (y.x > ki) + (y.y > ki);
