@@ -154,6 +154,37 @@ def selection_bytes(torch, ops, w: Workload):
                 total=b_cent + b_kv + b_q + b_out + b_meta, union_blocks_per_layer=u)
 
 
+def stream_copy_gbps(torch, nbytes: int = 1 << 30, reps: int = 10) -> float:
+    """Measured device copy bandwidth (read + write bytes / time) of a plain
+    torch copy of `nbytes`, the practical HBM ceiling next to the 8 TB/s peak."""
+    x = torch.empty(nbytes // 4, device="cuda", dtype=torch.float32).fill_(1.0)
+    y = torch.empty_like(x)
+    y.copy_(x)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        y.copy_(x)
+    e.record()
+    torch.cuda.synchronize()
+    gbps = 2 * nbytes * reps / (s.elapsed_time(e) * 1e-3) / 1e9
+    del x, y
+    return gbps
+
+
+def profiled_traffic(path: str):
+    """HBM bytes per launch of the centroid scan, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (calibrated against a plain copy); None if absent."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(torch, w: Workload, budget_s: float):
     """The NumPy oracle (reference.sparse_attention restated) on layer 0 of the
     same workload, single-threaded NumPy einsum; median seconds per layer."""
@@ -211,9 +242,14 @@ def main():
     g_sc = capture(torch, lambda l: w.scores(l, sbuf), L, stream)
     ms_sc, _ = time_graph(torch, g_sc, replays, warm)
     us_sc = ms_sc * 1e3 / steps
-    sc_bytes = nbytes["centroid"] + nbytes["q"]
+    sc_bytes = nbytes["centroid"] + nbytes["q"] + w.Hq * w.nb * 4      # centroids + q read, scores written
     sc_gbps = sc_bytes / (us_sc * 1e-6) / 1e9
     log(f"centroid scan: {us_sc:.2f} us/launch, {sc_gbps:.0f} GB/s")
+
+    copy_gbps = stream_copy_gbps(torch)
+    log(f"stream copy: {copy_gbps:.0f} GB/s")
+    traffic = profiled_traffic(os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                                            "score_kernel_128k_pmc.md"))
 
     dense_us = None
     if not args.no_dense:
@@ -249,10 +285,13 @@ def main():
         "roofline_frac_whole_op": round(gbps / PEAK_HBM_GBPS, 4),
         "dense_us_per_layer": None if dense_us is None else round(dense_us, 2),
         "speedup_vs_dense": None if dense_us is None else round(dense_us / us_layer, 2),
+        "stream_copy_GBps": round(copy_gbps, 1),
         "roofline": {"kernel": "score_kernel (centroid scan)", "bound": "hbm",
                      "achieved": round(sc_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": round(sc_gbps / PEAK_HBM_GBPS, 4), "traffic": None,
-                     "launch_us": round(us_sc, 3), "bytes_per_launch": int(sc_bytes)},
+                     "frac": round(sc_gbps / PEAK_HBM_GBPS, 4),
+                     "traffic": traffic if (traffic and args.ctx == 131072 and L == 32) else None,
+                     "launch_us": round(us_sc, 3), "bytes_per_launch": int(sc_bytes),
+                     "frac_of_stream_copy": round(sc_gbps / copy_gbps, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
