@@ -25,24 +25,17 @@
 
 #include "common.hpp"
 #include "internal.hpp"
+#include "select.hpp"
 
 namespace adakv {
 namespace {
 
 constexpr int kNT = 256;
-constexpr int kSortCap = 512;
 
 __device__ __forceinline__ float round_to(float x, int dt) {
   if (dt == ADAKV_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(x));
   if (dt == ADAKV_F16) return f16_bits_to_f32(f32_to_f16_bits(x));
   return x;
-}
-
-// NaN ranks last, infinities clamp to the finite range (they then tie with
-// +/-FLT_MAX and are ordered by block index).
-__device__ __forceinline__ float sanitize(float x) {
-  if (x != x) return -FLT_MAX;
-  return fminf(fmaxf(x, -FLT_MAX), FLT_MAX);
 }
 
 typedef float float4_t __attribute__((ext_vector_type(4)));
@@ -115,13 +108,13 @@ __device__ void append_block(const ScoreArgs& a, int b, int kvh, int r, int len,
   }
 }
 
-// Softmax partial of a chunk for one head, written by one lane: see the
-// PartRecord layout in internal.hpp.
-__device__ __forceinline__ void write_part(const ScoreArgs& a, int b, int h, int chunk, float m, float S, float T,
-                                           float lo, float hi) {
-  float4* rec = reinterpret_cast<float4*>(a.parts + (((int64_t)b * a.Hq + h) * a.parts_pitch + chunk) * kPartFloats);
-  rec[0] = make_float4(m, S, T, lo);
-  rec[1] = make_float4(hi, 0.f, 0.f, 0.f);
+// Softmax partial of a score workgroup's rows for one head, written by one
+// lane: m, S, T and the content maxima of the 4 sub-chunks (select.hpp).
+__device__ __forceinline__ void write_part(const ScoreArgs& a, int b, int h, int slot, float m, float S, float T,
+                                           float hi0, float hi1, float hi2, float hi3) {
+  float4* rec = reinterpret_cast<float4*>(a.parts + (((int64_t)b * a.Hq + h) * a.parts_pitch + slot) * kPartFloats);
+  rec[0] = make_float4(m, S, T, hi0);
+  rec[1] = make_float4(hi1, hi2, hi3, 0.f);
 }
 
 // fp32 centroids: one workgroup per chunk of CB blocks; every centroid row is
@@ -180,14 +173,15 @@ __device__ void score_chunk_valu(const ScoreArgs& a, int b, int kvh, int unit, i
   }
   if (a.parts == nullptr) return;
   // softmax partial of this chunk, one wave per q-head (adakv/budget.py:33-37 is
-  // then finished from the partials by the selection)
+  // then finished from the partials by the selection); the chunk is one
+  // sub-chunk for the content maxima
   constexpr int RL = (CB + kWave - 1) / kWave;   // rows per lane
   const Bounds bb = budget_bounds(nb, a.cfg);
   const int c_lo = bb.sink, c_hi = nb - bb.local;
   const float tf = (float)fmax(a.cfg.temperature, 1e-6);
   for (int g = w; g < G; g += kNT / kWave) {
     float z[RL];
-    float m = -INFINITY, lo = FLT_MAX, hi = -FLT_MAX;
+    float m = -INFINITY, hi = -INFINITY;
 #pragma unroll
     for (int k = 0; k < RL; ++k) {
       const int r = lane + k * kWave;
@@ -195,11 +189,7 @@ __device__ void score_chunk_valu(const ScoreArgs& a, int b, int kvh, int unit, i
       const float x = ok ? s_sc[g][r] : 0.f;
       z[k] = ok ? (tf == 1.f ? x : __fdiv_rn(x, tf)) : -INFINITY;
       m = fmaxf(m, z[k]);
-      if (ok && row0 + r >= c_lo && row0 + r < c_hi) {
-        const float xs = sanitize(x);
-        lo = fminf(lo, xs);
-        hi = fmaxf(hi, xs);
-      }
+      if (ok && row0 + r >= c_lo && row0 + r < c_hi) hi = fmaxf(hi, sanitize(x));
     }
     m = wave_allreduce(m, OpMax());
     float S = 0.f, T = 0.f;
@@ -215,9 +205,8 @@ __device__ void score_chunk_valu(const ScoreArgs& a, int b, int kvh, int unit, i
     }
     S = wave_allreduce(S, OpAdd());
     T = wave_allreduce(T, OpAdd());
-    lo = wave_allreduce(lo, OpMin());
     hi = wave_allreduce(hi, OpMax());
-    if (lane == 0) write_part(a, b, kvh * G + g, unit, m, S, T, lo, hi);
+    if (lane == 0) write_part(a, b, kvh * G + g, unit, m, S, T, hi, -INFINITY, -INFINITY, -INFINITY);
   }
 }
 
@@ -227,121 +216,147 @@ __device__ void score_chunk_valu(const ScoreArgs& a, int b, int kvh, int unit, i
 // loads issued at once), the group's q-heads, zero-padded to 16, form the B
 // operand.  Result lane (col, grp) holds the scores of rows 4*grp .. +3 of a
 // tile for head col: written as 16-byte stores, and reduced over the wave's
-// 64 rows into that head's softmax partial (one partial per wave).
+// 64 rows (one sub-chunk) into that head's softmax partial; the 4 waves'
+// partials are merged through LDS into the workgroup's record.
 template <int CDT, int D, int GMAX>
-__device__ void score_chunk_mfma(const ScoreArgs& a, int b, int kvh, int unit, int nb, int nrows) {
+__device__ void score_chunk_mfma(const ScoreArgs& a, int b, int kvh, int unit, int nb, int nrows,
+                                 float (*s_pm)[GMAX][4]) {
   static_assert(D % 32 == 0 && GMAX <= 16, "16x16 tiles over head_dim");
   constexpr int KS = D / 32;                // k-steps (16-byte loads per lane per tile)
   constexpr int TPW = 4;                    // tiles per wave
-  constexpr int RPW = 16 * TPW;             // rows per wave = rows per partial
+  constexpr int RPW = 16 * TPW;             // rows per wave = rows per sub-chunk
+  constexpr int NWV = kNT / kWave;
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const int col = lane & 15, grp = lane >> 4;
   const int G = a.G;
-  const int wrow0 = unit * (kNT / kWave) * RPW + w * RPW;
-  if (wrow0 >= nrows) return;
-  // A fragments: lane (col, grp) reads row wrow0 + 16t + col, elements [D/4*grp, D/4*(grp+1))
-  const char* cbase = reinterpret_cast<const char*>(a.c) +
-                      ((((int64_t)b * a.Hkv + kvh) * a.max_blocks) * D + (D / 4) * grp) * 2;
-  uint4 cf[TPW][KS];
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    const int r = min(wrow0 + 16 * t + col, nrows - 1);     // in bounds; extra rows masked below
-#pragma unroll
-    for (int s = 0; s < KS; ++s) cf[t][s] = load16(cbase + (int64_t)r * D * 2 + 16 * s);
-  }
-  // B fragments: lane (col, grp) holds q[head col][D/4*grp + 8s .. +7]
-  uint4 qf[KS];
-  with_dtype(a.qdt, [&](auto tag) {
-    constexpr int QDT = decltype(tag)::value;
-    const int64_t qo = (int64_t)b * a.qsb + (int64_t)(kvh * G + min(col, G - 1)) * a.qsh + (D / 4) * grp;
-    float x[KS][8];
-#pragma unroll
-    for (int s = 0; s < KS; ++s)
-#pragma unroll
-      for (int u = 0; u < 8; ++u) x[s][u] = load_t<QDT>(a.q, qo + 8 * s + u);
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      uint32_t wv[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) wv[u] = col < G ? pack2_typed<CDT>(x[s][2 * u], x[s][2 * u + 1]) : 0u;
-      qf[s] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
-    }
-  });
-  float sc[TPW][4];
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KS; ++s) acc = mfma_16x16x32<CDT>(cf[t][s], qf[s], acc);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sc[t][i] = acc[i];
-  }
-  // scores: rows 4*grp + i of each tile, head col
-  if (col < G) {
-    float* srow = a.scores + ((int64_t)b * a.Hq + kvh * G + col) * a.sp;
+  const int wrow0 = unit * NWV * RPW + w * RPW;
+  if (unit * NWV * RPW >= nrows) return;    // uniform over the workgroup
+  const bool wave_on = wrow0 < nrows;       // uniform over the wave
+  float m = -INFINITY, S = 0.f, T = 0.f, hi = -INFINITY;
+  if (wave_on) {
+    // A fragments: lane (col, grp) reads row wrow0 + 16t + col, elements [D/4*grp, D/4*(grp+1))
+    const char* cbase = reinterpret_cast<const char*>(a.c) +
+                        ((((int64_t)b * a.Hkv + kvh) * a.max_blocks) * D + (D / 4) * grp) * 2;
+    uint4 cf[TPW][KS];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      const int r = wrow0 + 16 * t + 4 * grp;
-      if (r + 3 < nrows) {
-        *reinterpret_cast<float4*>(srow + r) = make_float4(sc[t][0], sc[t][1], sc[t][2], sc[t][3]);
-      } else {
+      const int r = min(wrow0 + 16 * t + col, nrows - 1);     // in bounds; extra rows masked below
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (r + i < nrows) srow[r + i] = sc[t][i];
+      for (int s = 0; s < KS; ++s) cf[t][s] = load16(cbase + (int64_t)r * D * 2 + 16 * s);
+    }
+    // B fragments: lane (col, grp) holds q[head col][D/4*grp + 8s .. +7]
+    uint4 qf[KS];
+    with_dtype(a.qdt, [&](auto tag) {
+      constexpr int QDT = decltype(tag)::value;
+      const int64_t qo = (int64_t)b * a.qsb + (int64_t)(kvh * G + min(col, G - 1)) * a.qsh + (D / 4) * grp;
+      float x[KS][8];
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[s][u] = load_t<QDT>(a.q, qo + 8 * s + u);
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        uint32_t wv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) wv[u] = col < G ? pack2_typed<CDT>(x[s][2 * u], x[s][2 * u + 1]) : 0u;
+        qf[s] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+      }
+    });
+    float sc[TPW][4];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) acc = mfma_16x16x32<CDT>(cf[t][s], qf[s], acc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[t][i] = acc[i];
+    }
+    // scores: rows 4*grp + i of each tile, head col
+    if (col < G) {
+      float* srow = a.scores + ((int64_t)b * a.Hq + kvh * G + col) * a.sp;
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const int r = wrow0 + 16 * t + 4 * grp;
+        if (r + 3 < nrows) {
+          *reinterpret_cast<float4*>(srow + r) = make_float4(sc[t][0], sc[t][1], sc[t][2], sc[t][3]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (r + i < nrows) srow[r + i] = sc[t][i];
+        }
       }
     }
-  }
-  if (a.parts == nullptr) return;
-  // softmax partial of the wave's rows for head col (lanes col, col+16, col+32, col+48)
-  const Bounds bb = budget_bounds(nb, a.cfg);
-  const int c_lo = bb.sink, c_hi = nb - bb.local;
-  const float tf = (float)fmax(a.cfg.temperature, 1e-6);
-  // branch-free: content and validity are selects, empty rows contribute exp(-inf) = 0
-  float m = -INFINITY, lo = FLT_MAX, hi = -FLT_MAX;
+    if (a.parts == nullptr) return;
+    // softmax partial of the wave's rows for head col (lanes col, col+16, col+32, col+48)
+    const Bounds bb = budget_bounds(nb, a.cfg);
+    const int c_lo = bb.sink, c_hi = nb - bb.local;
+    const float tf = (float)fmax(a.cfg.temperature, 1e-6);
+    // branch-free: content and validity are selects, empty rows contribute exp(-inf) = 0
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) {
+    for (int t = 0; t < TPW; ++t) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = wrow0 + 16 * t + 4 * grp + i;
-      const bool cont = (r >= c_lo) & (r < c_hi) & (r < nrows);
-      const float xs = sanitize(sc[t][i]);
-      lo = fminf(lo, cont ? xs : FLT_MAX);
-      hi = fmaxf(hi, cont ? xs : -FLT_MAX);
+      for (int i = 0; i < 4; ++i) {
+        const int r = wrow0 + 16 * t + 4 * grp + i;
+        const bool cont = (r >= c_lo) & (r < c_hi) & (r < nrows);
+        hi = fmaxf(hi, cont ? sanitize(sc[t][i]) : -INFINITY);
+      }
     }
-  }
-  if (tf != 1.f) {   // temperature: the correctly rounded division only when it is needed (uniform)
+    if (tf != 1.f) {   // temperature: the correctly rounded division only when it is needed (uniform)
+#pragma unroll
+      for (int t = 0; t < TPW; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[t][i] = __fdiv_rn(sc[t][i], tf);
+    }
 #pragma unroll
     for (int t = 0; t < TPW; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sc[t][i] = __fdiv_rn(sc[t][i], tf);
+      for (int i = 0; i < 4; ++i) {
+        sc[t][i] = (wrow0 + 16 * t + 4 * grp + i < nrows) ? sc[t][i] : -INFINITY;
+        m = fmaxf(m, sc[t][i]);
+      }
+    LanePair pr = swap16(m);
+    m = fmaxf(pr.a, pr.b);
+    pr = swap32(m);
+    m = fmaxf(pr.a, pr.b);
+    const float mm = m == -INFINITY ? 0.f : m;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float dz = sc[t][i] - mm;
+        const float e = __expf(dz);
+        S += e;
+        T = fmaf(e, fmaxf(dz, -FLT_MAX), T);
+      }
+    pr = swap16(S); S = pr.a + pr.b; pr = swap32(S); S = pr.a + pr.b;
+    pr = swap16(T); T = pr.a + pr.b; pr = swap32(T); T = pr.a + pr.b;
+    pr = swap16(hi); hi = fmaxf(pr.a, pr.b); pr = swap32(hi); hi = fmaxf(pr.a, pr.b);
   }
+  if (a.parts == nullptr) return;           // uniform
+  if (grp == 0 && col < G) {
+    s_pm[w][col][0] = m; s_pm[w][col][1] = S; s_pm[w][col][2] = T; s_pm[w][col][3] = hi;
+  }
+  __syncthreads();
+  if (w == 0 && lane < G) {
+    // the workgroup's record: the 4 sub-chunk partials rescaled to their common max
+    float M = -INFINITY;
 #pragma unroll
-  for (int t = 0; t < TPW; ++t)
+    for (int ww = 0; ww < NWV; ++ww) M = fmaxf(M, s_pm[ww][lane][0]);
+    float SS = 0.f, TT = 0.f;
+    if (M != -INFINITY) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sc[t][i] = (wrow0 + 16 * t + 4 * grp + i < nrows) ? sc[t][i] : -INFINITY;
-      m = fmaxf(m, sc[t][i]);
+      for (int ww = 0; ww < NWV; ++ww) {
+        const float mw = s_pm[ww][lane][0];
+        if (mw != -INFINITY) {
+          const float d = mw - M, f = __expf(d);
+          SS += s_pm[ww][lane][1] * f;
+          TT += f * fmaf(d, s_pm[ww][lane][1], s_pm[ww][lane][2]);
+        }
+      }
     }
-  LanePair pr = swap16(m);
-  m = fmaxf(pr.a, pr.b);
-  pr = swap32(m);
-  m = fmaxf(pr.a, pr.b);
-  const float mm = m == -INFINITY ? 0.f : m;
-  float S = 0.f, T = 0.f;
-#pragma unroll
-  for (int t = 0; t < TPW; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float dz = sc[t][i] - mm;
-      const float e = __expf(dz);
-      S += e;
-      T = fmaf(e, fmaxf(dz, -FLT_MAX), T);
-    }
-  pr = swap16(S); S = pr.a + pr.b; pr = swap32(S); S = pr.a + pr.b;
-  pr = swap16(T); T = pr.a + pr.b; pr = swap32(T); T = pr.a + pr.b;
-  pr = swap16(lo); lo = fminf(pr.a, pr.b); pr = swap32(lo); lo = fminf(pr.a, pr.b);
-  pr = swap16(hi); hi = fmaxf(pr.a, pr.b); pr = swap32(hi); hi = fmaxf(pr.a, pr.b);
-  if (grp == 0 && col < G) write_part(a, b, kvh * G + col, wrow0 / RPW, m, S, T, lo, hi);
+    write_part(a, b, kvh * G + lane, unit, M, SS, TT, s_pm[0][lane][3], s_pm[1][lane][3], s_pm[2][lane][3],
+               s_pm[3][lane][3]);
+  }
 }
 
 // Scores of every block of every (sequence, KV head) against its G q-heads.
@@ -355,6 +370,7 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
   __shared__ float s_q[GMAX][D];
   __shared__ float s_sc[kMfma ? 1 : GMAX * CBV];
   __shared__ float s_red[GMAX][kNT / kWave];
+  __shared__ float s_pm[kNT / kWave][GMAX][4];
 
   int id = blockIdx.x;
   const bool app = id < a.n_app * a.Hkv * a.B;
@@ -380,7 +396,7 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
   }
   const int nrows = min(nb, first_app);     // appended blocks are scored by their own workgroups
   if constexpr (kMfma) {
-    score_chunk_mfma<CDT, D, GMAX>(a, b, kvh, unit, nb, nrows);
+    score_chunk_mfma<CDT, D, GMAX>(a, b, kvh, unit, nb, nrows, s_pm);
   } else {
     if (unit * CBV >= nrows) return;
     score_chunk_valu<CDT, D, GMAX>(a, b, kvh, unit, nb, nrows, s_q, s_sc);
@@ -388,151 +404,14 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
 }
 
 // ------------------------------------------------------------- selection ----
-// Order-preserving map of a (sanitised) float to uint32 plus the block index,
-// so that larger score, then smaller index, gives the larger key.
-__device__ __forceinline__ uint64_t sel_key(float x, int idx) {
-  uint32_t u = __float_as_uint(x);
-  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((uint64_t)u << 32) | (uint32_t)(0xffffffffu - (uint32_t)idx);
-}
-__device__ __forceinline__ int key_index(uint64_t k) {
-  return (int)(0xffffffffu - (uint32_t)(k & 0xffffffffu));
-}
-
-// Bitonic sort of s_keys[0, n) into descending order; n a power of two <= kSortCap.
-template <int NT>
-__device__ void bitonic_desc(uint64_t* s_keys, int n) {
-  for (int k = 2; k <= n; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < n; i += NT) {
-        const int ixj = i ^ j;
-        if (ixj > i) {
-          const uint64_t x = s_keys[i], y = s_keys[ixj];
-          const bool desc = (i & k) == 0;
-          if (desc ? (x < y) : (x > y)) {
-            s_keys[i] = y;
-            s_keys[ixj] = x;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
-}
-
-__device__ __forceinline__ int next_pow2(int n) {
-  int p = 1;
-  while (p < n) p <<= 1;
-  return p;
-}
-
-template <int IPT>
-using MaskT = typename std::conditional<(IPT > 32), uint64_t, uint32_t>::type;
-
-template <typename M>
-__device__ __forceinline__ int popcnt(M m) {
-  if constexpr (sizeof(M) == 8) return __popcll(m); else return __popc(m);
-}
-
-// Softmax partial (see PartRecord layout) and its merge: the larger max wins,
-// the other side's sums are rescaled by exp(m' - M); T picks up (m' - M) * S'.
-struct Part {
-  float m, S, T, lo, hi;
-};
-__device__ __forceinline__ Part part_empty() { return Part{-INFINITY, 0.f, 0.f, FLT_MAX, -FLT_MAX}; }
-__device__ __forceinline__ Part part_merge(const Part& x, const Part& y) {
-  Part r;
-  r.m = fmaxf(x.m, y.m);
-  r.lo = fminf(x.lo, y.lo);
-  r.hi = fmaxf(x.hi, y.hi);
-  if (r.m == -INFINITY) { r.S = 0.f; r.T = 0.f; return r; }
-  const float dx = x.m - r.m, dy = y.m - r.m;
-  const float fx = x.m == -INFINITY ? 0.f : __expf(dx), fy = y.m == -INFINITY ? 0.f : __expf(dy);
-  r.S = x.S * fx + y.S * fy;
-  r.T = (x.m == -INFINITY ? 0.f : fx * fmaf(dx, x.S, x.T)) + (y.m == -INFINITY ? 0.f : fy * fmaf(dy, y.S, y.T));
-  return r;
-}
-template <int CTRL>
-__device__ __forceinline__ Part part_dpp(const Part& p) {
-  return Part{dpp_mov<CTRL>(p.m), dpp_mov<CTRL>(p.S), dpp_mov<CTRL>(p.T), dpp_mov<CTRL>(p.lo), dpp_mov<CTRL>(p.hi)};
-}
-// Merge over the 64 lanes; every lane receives the result.
-__device__ __forceinline__ Part part_wave_merge(Part p) {
-  p = part_merge(p, part_dpp<0xB1>(p));
-  p = part_merge(p, part_dpp<0x4E>(p));
-  p = part_merge(p, part_dpp<0x141>(p));
-  p = part_merge(p, part_dpp<0x140>(p));
-  {
-    const LanePair a = swap16(p.m), b = swap16(p.S), c = swap16(p.T), d = swap16(p.lo), e = swap16(p.hi);
-    p = part_merge(Part{a.a, b.a, c.a, d.a, e.a}, Part{a.b, b.b, c.b, d.b, e.b});
-  }
-  {
-    const LanePair a = swap32(p.m), b = swap32(p.S), c = swap32(p.T), d = swap32(p.lo), e = swap32(p.hi);
-    p = part_merge(Part{a.a, b.a, c.a, d.a, e.a}, Part{a.b, b.b, c.b, d.b, e.b});
-  }
-  return p;
-}
-
-// Normalised entropy weight of head h (adakv/budget.py:33-37), by one wave
-// from the per-wave softmax partials: sum p log p = T / S - log S.
-template <int NW>
-__device__ __forceinline__ void write_weight(const SelectArgs& a, int b, int h, int nb, bool adaptive,
-                                             const float (*s_r)[5]) {
-  if (!adaptive) return;
-  const int lane = threadIdx.x & (kWave - 1);
-  const bool ok = lane < NW;
-  const float m = ok ? s_r[lane][0] : -INFINITY;
-  const float M = wave_allreduce(m, OpMax());
-  float S = 0.f, T = 0.f;
-  if (m != -INFINITY) {
-    const float d = m - M, f = __expf(d);
-    S = s_r[lane][1] * f;
-    T = f * fmaf(d, s_r[lane][1], s_r[lane][2]);
-  }
-  S = wave_allreduce(S, OpAdd());
-  T = wave_allreduce(T, OpAdd());
-  if (lane == 0) {
-    const float hs = T / S - __logf(S);
-    a.wbuf[(int64_t)b * a.Hq + h] = (double)(-hs) / log((double)max(nb, 2)) + 1e-6;
-  }
-}
-
-// One wave: the digit d of a 256-bin histogram (bins indexed by digit, larger
-// digit = larger key) that holds the need-th largest key; out[0] = d, out[1] =
-// keys in larger digits.  out[1] = -1 when the histogram holds fewer than need keys.
-__device__ __forceinline__ void radix_digit(const int* hist, int need, int* out) {
-  const int lane = threadIdx.x & (kWave - 1);
-  int c4[4], s4 = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) { c4[j] = hist[255 - (4 * lane + j)]; s4 += c4[j]; }
-  const int inc = wave_incl_scan(s4);
-  const int tot = __builtin_amdgcn_readlane(inc, kWave - 1);
-  int before = inc - s4;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (before < need && need <= before + c4[j]) { out[0] = 255 - (4 * lane + j); out[1] = before; }
-    before += c4[j];
-  }
-  if (lane == 0 && (tot < need || need <= 0)) { out[0] = 0; out[1] = -1; }
-}
-
 template <int NT, int IPT>
 __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
   static_assert(IPT <= 64 && IPT % 4 == 0 && NT >= 256, "one mask word per thread");
   constexpr int NW = NT / kWave;
   using Mask = MaskT<IPT>;
   constexpr Mask kOne = 1;
-  __shared__ __align__(16) uint64_t s_keys[kSortCap];
-  __shared__ int s_hist[256];
-  __shared__ float s_r[NW][5];
-  __shared__ int s_rank[kSortCap];
-  __shared__ __align__(16) float s_max[NT];   // chunk content maxima (+ appended rows)
-  __shared__ float s_tau;
-  __shared__ int s_rh[512];             // two radix histograms for the threshold
-  __shared__ float s_f[NW];
-  __shared__ int s_i[NW];
-  __shared__ int s_bc[4];
-  __shared__ int s_n;
+  __shared__ SelectLds<NT> L;
+  __shared__ float s_r[NW][3];
 
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & (kWave - 1), w = tid / kWave;
@@ -543,9 +422,7 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
   const int n_content = max(c_hi - c_lo, 0);
   const int KC = min(max(bb.kcap - bb.n_forced, 0), n_content);
   const bool adaptive = a.cfg.policy == ADAKV_POLICY_ADAPTIVE && nb > 1;
-  if (tid == 0) { s_n = 0; s_tau = -FLT_MAX; }
-  for (int i = tid; i < kSortCap; i += NT) s_rank[i] = 0;
-  for (int i = tid; i < 512; i += NT) s_rh[i] = 0;
+  select_init(L);
 
   // ---- forced prefix and padding of the block-table row ----
   int32_t* trow = a.table + ((int64_t)b * a.Hq + h) * a.T;
@@ -557,35 +434,28 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
   const float* srow = a.scores + ((int64_t)b * a.Hq + h) * a.sp;
   const int base = tid * IPT;
   float v[IPT];
-#pragma unroll
-  for (int i = 0; i < IPT; i += 4) {
-    if (base + i + 3 < nb) {
-      const float4 f = *reinterpret_cast<const float4*>(srow + base + i);
-      v[i] = f.x; v[i + 1] = f.y; v[i + 2] = f.z; v[i + 3] = f.w;
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[i + j] = (base + i + j < nb) ? srow[base + i + j] : 0.f;
-    }
-  }
+  load_scores(srow, nb, v);
 
-  // ---- softmax partials: the score kernel's chunks plus the rows it left out ----
+  // ---- softmax partials: the score kernel's records plus the rows it left out ----
   // (blocks recomputed by the decode-time append are scored on their own and
-  // belong to no chunk; each counts as a one-row chunk here).  A wave first
-  // takes the max, rescales its lanes' sums to it once, then adds.
+  // belong to no record; each counts as a one-row part here).  Sub-chunk
+  // content maxima go to L.maxv: 4 per record, then one per left-out row.
   const int first_app = a.n_new > 0 ? max(len - a.n_new, 0) / a.bs : nb;
   const int rows_in_chunks = min(nb, first_app);
-  const int n_chunks = ceil_div(rows_in_chunks, a.chunk_rows);
+  const int n_ck = ceil_div(rows_in_chunks, a.chunk_rows);
   const float tf = (float)fmax(a.cfg.temperature, 1e-6);
   const bool unit = tf == 1.f;
-  Part pt = part_empty();
+  SoftPart pt = soft_empty();
   bool has = false;
-  for (int c = tid; c < n_chunks; c += NT) {
+  for (int c = tid; c < n_ck; c += NT) {
     const float4* rec = reinterpret_cast<const float4*>(a.parts + (((int64_t)b * a.Hq + h) * a.parts_pitch + c) *
                                                                   kPartFloats);
     const float4 r0 = rec[0], r1 = rec[1];
-    pt = part_merge(pt, Part{r0.x, r0.y, r0.z, r0.w, r1.x});
-    // content maximum of the chunk (none: -inf); chunks past NT are not counted
-    if (c < NT) s_max[c] = (r1.x == -FLT_MAX && r0.w == FLT_MAX) ? -INFINITY : r1.x;
+    pt = soft_merge(pt, SoftPart{r0.x, r0.y, r0.z});
+    const float mx[4] = {r0.w, r1.x, r1.y, r1.z};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (4 * c + i < NT) L.maxv[4 * c + i] = mx[i];
     has = true;
   }
   Mask content = 0;
@@ -596,220 +466,26 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
     if (is_content) content |= kOne << i;
     if (idx >= rows_in_chunks && idx < nb) {
       const float z = unit ? v[i] : __fdiv_rn(v[i], tf);
-      const float xs = sanitize(v[i]);
-      pt = part_merge(pt, Part{z, 1.f, 0.f, is_content ? xs : FLT_MAX, is_content ? xs : -FLT_MAX});
-      const int t = n_chunks + idx - rows_in_chunks;
-      if (t < NT) s_max[t] = is_content ? xs : -INFINITY;
+      pt = soft_merge(pt, SoftPart{z, 1.f, 0.f});
+      const int t = 4 * n_ck + idx - rows_in_chunks;
+      if (t < NT) L.maxv[t] = is_content ? sanitize(v[i]) : -INFINITY;
       has = true;
     }
   }
-  const int n_max = min(n_chunks + (nb - rows_in_chunks), NT);
-  if (tid >= n_max && tid < ((n_max + 3) & ~3)) s_max[tid] = -INFINITY;
-  if (__ballot(has) != 0) {                    // waves without partials skip the reductions
-    const float M = wave_allreduce(pt.m, OpMax());
-    float S = 0.f, T = 0.f;
-    if (pt.m != -INFINITY) {
-      const float d = pt.m - M, f = __expf(d);
-      S = pt.S * f;
-      T = f * fmaf(d, pt.S, pt.T);
-    }
-    pt = Part{M, wave_allreduce(S, OpAdd()), wave_allreduce(T, OpAdd()), wave_allreduce(pt.lo, OpMin()),
-              wave_allreduce(pt.hi, OpMax())};
-  }
-  if (lane == 0) { s_r[w][0] = pt.m; s_r[w][1] = pt.S; s_r[w][2] = pt.T; s_r[w][3] = pt.lo; s_r[w][4] = pt.hi; }
-  __syncthreads();
-  if (KC <= 0) {
-    if (w == NW - 1) write_weight<NW>(a, b, h, nb, adaptive, s_r);
-    return;
-  }
-
-  // ---- selection threshold tau from the chunk content maxima ----
-  // Two radix passes over the order-preserving keys of the maxima (top byte,
-  // then the next byte within the bin that holds the KC-th largest) give the
-  // 16-bit key prefix of the KC-th largest maximum; tau is the smallest float
-  // with that prefix.  At least KC content scores (those maxima) are >= tau,
-  // so every one of the top KC is; missing maxima only lower tau.
-  {
-    const bool has_max = tid < n_max && s_max[tid] != -INFINITY;
-    const uint32_t key = has_max ? (uint32_t)(sel_key(s_max[tid], 0) >> 32) : 0u;
-    if (has_max) atomicAdd(&s_rh[key >> 24], 1);
-    __syncthreads();
-    if (w == 0) radix_digit(s_rh, KC, s_bc);          // s_bc[0] = digit, s_bc[1] = count above
-    __syncthreads();
-    const uint32_t b1 = (uint32_t)s_bc[0];
-    const int above1 = s_bc[1];
-    if (has_max && (key >> 24) == b1) atomicAdd(&s_rh[256 + ((key >> 16) & 0xffu)], 1);
-    __syncthreads();
-    if (w == 0) {
-      radix_digit(s_rh + 256, KC - above1, s_bc + 2);
-      if (lane == 0) {
-        const uint32_t tk = (b1 << 24) | ((uint32_t)s_bc[2] << 16);
-        const uint32_t u = (tk & 0x80000000u) ? (tk & 0x7fffffffu) : ~tk;
-        s_tau = (above1 < 0 || s_bc[3] < 0) ? -FLT_MAX : fmaxf(__uint_as_float(u), -FLT_MAX);
-      }
-    }
-  }
+  const int n_max = min(4 * n_ck + (nb - rows_in_chunks), NT);
+  if (__ballot(has) != 0) pt = soft_group_merge<kWave>(pt);   // waves without partials skip the merge
+  if (lane == 0) { s_r[w][0] = pt.m; s_r[w][1] = pt.S; s_r[w][2] = pt.T; }
   __syncthreads();
 
-  // ---- candidates: content scores >= tau, one LDS atomic per wave ----
-  const float tau = s_tau;
-  Mask cm = 0;
-  if (tau == -FLT_MAX) {                       // the bottom of the range: compare sanitised scores
-#pragma unroll
-    for (int i = 0; i < IPT; ++i) cm |= (sanitize(v[i]) >= tau) ? (kOne << i) : Mask(0);
-  } else {
-#pragma unroll
-    for (int i = 0; i < IPT; ++i) cm |= (v[i] >= tau) ? (kOne << i) : Mask(0);
+  if (KC > 0) {
+    const int nf = bb.n_forced;
+    select_content<NT, IPT>(L, v, content, base, KC, n_max, [&](int r, int blk) { trow[nf + r] = blk; });
   }
-  cm &= content;
-  {
-    const int c = popcnt(cm);
-    const int inc = wave_incl_scan(c);
-    const int wtot = __builtin_amdgcn_readlane(inc, kWave - 1);
-    if (wtot) {
-      int o0 = 0;
-      if (lane == kWave - 1) o0 = atomicAdd(&s_n, wtot);
-      int o = __builtin_amdgcn_readlane(o0, kWave - 1) + inc - c;
-#pragma unroll
-      for (int i = 0; i < IPT; ++i) {
-        const bool bit = (cm >> i) & kOne;
-        if (__ballot(bit)) {                   // most element positions hold no candidate in the wave
-          if (bit && o < kSortCap) s_keys[o] = sel_key(sanitize(v[i]), base + i);
-          o += bit ? 1 : 0;
-        }
-      }
-    }
-  }
-  __syncthreads();
-  const int n_cand = s_n;
-  if (n_cand <= kSortCap) {
-    // rank every candidate against all others, the pairs spread over the workgroup
-    if (tid == 0 && (n_cand & 1)) s_keys[n_cand] = 0;   // pad to pairs: key 0 ranks below every key
-    __syncthreads();
-    const int n2 = (n_cand + 1) & ~1;
-    const int npad = next_pow2(max(n_cand, 1));
-    const int parts = max(NT / npad, 1), jlen = (ceil_div(n2, parts) + 1) & ~1;
-    const int i = tid % npad, j0 = (tid / npad) * jlen, j1 = min(n2, j0 + jlen);
-    if (i < n_cand && tid / npad < parts) {
-      const uint64_t ki = s_keys[i];
-      int r = 0;
-#pragma unroll 4
-      for (int j = j0; j < j1; j += 2) {
-        const ulonglong2 y = *reinterpret_cast<const ulonglong2*>(&s_keys[j]);
-        r += (y.x > ki) + (y.y > ki);
-      }
-      if (r) atomicAdd(&s_rank[i], r);
-    }
-    __syncthreads();
-    for (int e = tid; e < n_cand; e += NT)
-      if (s_rank[e] < KC) trow[bb.n_forced + s_rank[e]] = key_index(s_keys[e]);
-    if (w == NW - 1) write_weight<NW>(a, b, h, nb, adaptive, s_r);
-    return;
-  }
-  if (w == NW - 1) write_weight<NW>(a, b, h, nb, adaptive, s_r);
-#pragma unroll
-  for (int i = 0; i < IPT; ++i)
-    if ((content >> i) & kOne) v[i] = sanitize(v[i]);
-
-  // ---- fallback: the boundary bin holds too many blocks; refine exactly ----
-  Mask cand = content, sel = 0;
-  int need = KC, nsel = 0;
-  bool sort_union = false;
-  for (;;) {
-    const int cnt = block_reduce<NT>(popcnt(cand), s_i, OpAdd());
-    if (need <= 0) { cand = 0; break; }
-    if (need >= cnt) { sel |= cand; cand = 0; nsel += cnt; need = 0; break; }
-    if (nsel + cnt <= kSortCap) { sort_union = true; break; }
-    if (cnt <= kSortCap) {
-      int tot;
-      const int off = block_excl_scan<NT>(popcnt(cand), s_i, &tot);
-      int o = off;
-#pragma unroll
-      for (int i = 0; i < IPT; ++i)
-        if ((cand >> i) & kOne) s_keys[o++] = sel_key(v[i], base + i);
-      const int n = next_pow2(tot);
-      for (int i = tot + tid; i < n; i += NT) s_keys[i] = 0;
-      __syncthreads();
-      bitonic_desc<NT>(s_keys, n);
-      const uint64_t kth = s_keys[need - 1];
-#pragma unroll
-      for (int i = 0; i < IPT; ++i)
-        if (((cand >> i) & kOne) && sel_key(v[i], base + i) >= kth) sel |= kOne << i;
-      nsel += need; need = 0; cand = 0;
-      __syncthreads();
-      break;
-    }
-    float lo2 = FLT_MAX, hi2 = -FLT_MAX;
-#pragma unroll
-    for (int i = 0; i < IPT; ++i)
-      if ((cand >> i) & kOne) { lo2 = fminf(lo2, v[i]); hi2 = fmaxf(hi2, v[i]); }
-    lo2 = block_reduce<NT>(lo2, s_f, OpMin());
-    hi2 = block_reduce<NT>(hi2, s_f, OpMax());
-    if (lo2 == hi2) {
-      // all candidates tie: take the lowest block indices
-      int tot;
-      const int off = block_excl_scan<NT>(popcnt(cand), s_i, &tot);
-      int r = off;
-#pragma unroll
-      for (int i = 0; i < IPT; ++i)
-        if ((cand >> i) & kOne) { if (r < need) sel |= kOne << i; ++r; }
-      nsel += need; need = 0; cand = 0;
-      break;
-    }
-    // 256 linear bins in double precision: vhi2 and vlo2 always land in
-    // different bins, so the candidate set shrinks on every pass
-    const double inv = 256.0 / ((double)hi2 - (double)lo2);
-    auto bin2 = [&](float x) { return (int)fmin(255.0, floor(((double)hi2 - (double)x) * inv)); };
-    for (int i = tid; i < 256; i += NT) s_hist[i] = 0;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < IPT; ++i)
-      if ((cand >> i) & kOne) atomicAdd(&s_hist[bin2(v[i])], 1);
-    __syncthreads();
-    if (tid < kWave) {
-      int c4[4], s4 = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) { c4[j] = s_hist[4 * tid + j]; s4 += c4[j]; }
-      int before = wave_incl_scan(s4) - s4;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (before < need && need <= before + c4[j]) { s_bc[2] = 4 * tid + j; s_bc[3] = before; }
-        before += c4[j];
-      }
-    }
-    __syncthreads();
-    const int bs2 = s_bc[2], above = s_bc[3];
-#pragma unroll
-    for (int i = 0; i < IPT; ++i) {
-      if ((cand >> i) & kOne) {
-        const int bi = bin2(v[i]);
-        if (bi < bs2) { sel |= kOne << i; cand &= ~(kOne << i); }
-        else if (bi > bs2) cand &= ~(kOne << i);
-      }
-    }
-    nsel += above;
-    need -= above;
-    __syncthreads();
-  }
-  const Mask outm = sort_union ? (sel | cand) : sel;
-  int tot;
-  const int off = block_excl_scan<NT>(popcnt(outm), s_i, &tot);
-  if (sort_union || KC <= kSortCap) {
-    int o = off;
-#pragma unroll
-    for (int i = 0; i < IPT; ++i)
-      if ((outm >> i) & kOne) s_keys[o++] = sel_key(v[i], base + i);
-    const int n = next_pow2(tot);
-    for (int i = tot + tid; i < n; i += NT) s_keys[i] = 0;
-    __syncthreads();
-    bitonic_desc<NT>(s_keys, n);
-    for (int j = tid; j < KC; j += NT) trow[bb.n_forced + j] = key_index(s_keys[j]);
-  } else {
-    // more than kSortCap content blocks: listed in block order
-    int o = off;
-#pragma unroll
-    for (int i = 0; i < IPT; ++i)
-      if ((outm >> i) & kOne) trow[bb.n_forced + o++] = base + i;
+  // the head's entropy weight from the waves' partials (adakv/budget.py:33-37)
+  if (adaptive && w == NW - 1) {
+    SoftPart p = lane < NW ? SoftPart{s_r[lane][0], s_r[lane][1], s_r[lane][2]} : soft_empty();
+    p = soft_group_merge<kWave>(p);
+    if (lane == 0) a.wbuf[(int64_t)b * a.Hq + h] = entropy_weight(p, nb);
   }
 }
 
@@ -840,8 +516,8 @@ hipError_t launch_score_d(ScoreArgs& a, hipStream_t s) {
     a.chunk_rows = CB;
     a.n_chunks = (a.max_blocks + CB - 1) / CB;
   } else {
-    a.chunk_rows = 64;                                          // rows per wave = rows per partial
-    a.n_chunks = (a.max_blocks + 4 * 64 - 1) / (4 * 64);        // 4 waves per workgroup
+    a.chunk_rows = 4 * 64;                                      // 4 waves of 64 rows per record
+    a.n_chunks = (a.max_blocks + 4 * 64 - 1) / (4 * 64);
   }
   // blocks holding the newest n_new tokens: at most ceil(n_new / bs) + 1
   a.n_app = a.n_new > 0 ? std::min((a.n_new + a.bs - 1) / a.bs + 1, a.max_blocks) : 0;

@@ -1,0 +1,386 @@
+// Top-k content selection of one head inside one workgroup, shared by the
+// plan-only selection kernel and the fused selection + decode kernel
+// (adakv/selector.py:18-60: content blocks by descending score, ties by the
+// lower block index), and the mergeable softmax partials the entropy weights
+// are built from (adakv/budget.py:31-37).
+#pragma once
+
+#include <float.h>
+
+#include <type_traits>
+
+#include "common.hpp"
+
+namespace adakv {
+
+constexpr int kSortCap = 512;       // candidates ranked exactly by all-pairs comparison
+
+// NaN ranks last, infinities clamp to the finite range (they then tie with
+// +/-FLT_MAX and are ordered by block index).
+__device__ __forceinline__ float sanitize(float x) {
+  if (x != x) return -FLT_MAX;
+  return fminf(fmaxf(x, -FLT_MAX), FLT_MAX);
+}
+
+// Order-preserving map of a (sanitised) float to uint32 plus the block index,
+// so that larger score, then smaller index, gives the larger key.
+__device__ __forceinline__ uint64_t sel_key(float x, int idx) {
+  uint32_t u = __float_as_uint(x);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint32_t)(0xffffffffu - (uint32_t)idx);
+}
+__device__ __forceinline__ int key_index(uint64_t k) {
+  return (int)(0xffffffffu - (uint32_t)(k & 0xffffffffu));
+}
+
+// Bitonic sort of keys[0, n) into descending order; n a power of two <= kSortCap.
+template <int NT>
+__device__ void bitonic_desc(uint64_t* keys, int n) {
+  for (int k = 2; k <= n; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < n; i += NT) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const uint64_t x = keys[i], y = keys[ixj];
+          const bool desc = (i & k) == 0;
+          if (desc ? (x < y) : (x > y)) {
+            keys[i] = y;
+            keys[ixj] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__device__ __forceinline__ int next_pow2(int n) {
+  int p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+template <int IPT>
+using MaskT = typename std::conditional<(IPT > 32), uint64_t, uint32_t>::type;
+
+template <typename M>
+__device__ __forceinline__ int popcnt(M m) {
+  if constexpr (sizeof(M) == 8) return __popcll(m); else return __popc(m);
+}
+
+// ---- softmax partials ------------------------------------------------------
+// Partial of a set of a head's scores z = score / temperature: m = max z,
+// S = sum exp(z - m), T = sum exp(z - m) * (z - m).  Two partials merge by
+// rescaling both to the larger max: T picks up (m' - M) * S'.  Then
+// sum p log p = T / S - log S over the whole set.
+//
+// Record written by the score kernel per (sequence, q-head, score workgroup),
+// kPartFloats floats: m, S, T, then the content maxima of the workgroup's 4
+// sub-chunks (-inf: no content block in the sub-chunk), then one unused float.
+struct SoftPart {
+  float m, S, T;
+};
+__device__ __forceinline__ SoftPart soft_empty() { return SoftPart{-INFINITY, 0.f, 0.f}; }
+__device__ __forceinline__ SoftPart soft_merge(const SoftPart& x, const SoftPart& y) {
+  const float M = fmaxf(x.m, y.m);
+  if (M == -INFINITY) return soft_empty();
+  const float dx = x.m - M, dy = y.m - M;
+  const float fx = x.m == -INFINITY ? 0.f : __expf(dx), fy = y.m == -INFINITY ? 0.f : __expf(dy);
+  return SoftPart{M, x.S * fx + y.S * fy,
+                  (x.m == -INFINITY ? 0.f : fx * fmaf(dx, x.S, x.T)) + (y.m == -INFINITY ? 0.f : fy * fmaf(dy, y.S, y.T))};
+}
+
+// Merge over aligned groups of N lanes (N = 32 or 64): the max first, then
+// every lane rescales its sums to it once and the sums are added.
+template <int N>
+__device__ __forceinline__ SoftPart soft_group_merge(SoftPart p) {
+  static_assert(N == 32 || N == 64, "half-wave or wave groups");
+  float M = p.m;
+  M = fmaxf(M, dpp_mov<0xB1>(M));
+  M = fmaxf(M, dpp_mov<0x4E>(M));
+  M = fmaxf(M, dpp_mov<0x141>(M));
+  M = fmaxf(M, dpp_mov<0x140>(M));
+  { const LanePair q = swap16(M); M = fmaxf(q.a, q.b); }
+  if constexpr (N == 64) { const LanePair q = swap32(M); M = fmaxf(q.a, q.b); }
+  float S = 0.f, T = 0.f;
+  if (p.m != -INFINITY) {
+    const float d = p.m - M, f = __expf(d);
+    S = p.S * f;
+    T = f * fmaf(d, p.S, p.T);
+  }
+  return SoftPart{M, group_sum<N>(S), group_sum<N>(T)};
+}
+
+// Normalised entropy weight (adakv/budget.py:33-37) from the merged partial of
+// all of a head's scores: -sum p log p / log(max(nb, 2)) + 1e-6, in fp64 after
+// the division as NumPy promotes it.
+__device__ __forceinline__ double entropy_weight(const SoftPart& p, int nb) {
+  const float hs = p.T / p.S - __logf(p.S);
+  return (double)(-hs) / log((double)max(nb, 2)) + 1e-6;
+}
+
+// ---- the selection ---------------------------------------------------------
+template <int NT>
+struct SelectLds {
+  alignas(16) uint64_t keys[kSortCap];
+  int hist[256];
+  int rank[kSortCap];
+  alignas(16) float maxv[NT];   // content maxima of sub-chunks (upper bounds for the threshold)
+  int rh[512];                  // two radix histograms for the threshold
+  float f[NT / kWave];
+  int i[NT / kWave];
+  int bc[4];
+  float tau;
+  int n;
+};
+
+// Clears what select_content expects to start at zero; before the first barrier.
+template <int NT>
+__device__ __forceinline__ void select_init(SelectLds<NT>& L) {
+  const int tid = threadIdx.x;
+  if (tid == 0) { L.n = 0; L.tau = -FLT_MAX; }
+  for (int i = tid; i < kSortCap; i += NT) L.rank[i] = 0;
+  for (int i = tid; i < 512; i += NT) L.rh[i] = 0;
+}
+
+// The head's scores: thread t owns blocks [t*IPT, (t+1)*IPT); blocks >= nb read 0.
+template <int IPT>
+__device__ __forceinline__ void load_scores(const float* srow, int nb, float (&v)[IPT]) {
+  const int base = threadIdx.x * IPT;
+#pragma unroll
+  for (int i = 0; i < IPT; i += 4) {
+    if (base + i + 3 < nb) {
+      const float4 f = *reinterpret_cast<const float4*>(srow + base + i);
+      v[i] = f.x; v[i + 1] = f.y; v[i + 2] = f.z; v[i + 3] = f.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[i + j] = (base + i + j < nb) ? srow[base + i + j] : 0.f;
+    }
+  }
+}
+
+// One wave: the digit d of a 256-bin histogram (bins indexed by digit, larger
+// digit = larger key) that holds the need-th largest key; out[0] = d, out[1] =
+// keys in larger digits.  out[1] = -1 when the histogram holds fewer than need keys.
+__device__ __forceinline__ void radix_digit(const int* hist, int need, int* out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int c4[4], s4 = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { c4[j] = hist[255 - (4 * lane + j)]; s4 += c4[j]; }
+  const int inc = wave_incl_scan(s4);
+  const int tot = __builtin_amdgcn_readlane(inc, kWave - 1);
+  int before = inc - s4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (before < need && need <= before + c4[j]) { out[0] = 255 - (4 * lane + j); out[1] = before; }
+    before += c4[j];
+  }
+  if (lane == 0 && (tot < need || need <= 0)) { out[0] = 0; out[1] = -1; }
+}
+
+// The KC largest content scores of a head, by (score desc, block asc), with
+// NaN ranked last and infinities clamped (sanitize).  Thread t holds the
+// scores of blocks [base, base + IPT) in v and their content bits in
+// `content`; L.maxv[0, n_max) (n_max <= NT) holds the content maxima of
+// disjoint sub-chunks (or -inf), written before a barrier, and L is
+// select_init'ed.  Calls emit(r, block) for every rank r < KC (KC >= 1).
+// Called by all NT threads.
+//
+// A threshold tau comes first: two radix passes over the order-preserving
+// keys of the maxima (top byte, then the next byte within the bin that holds
+// the KC-th largest) give the 16-bit key prefix of the KC-th largest maximum;
+// tau is the smallest float with that prefix.  Those KC maxima are KC distinct
+// content scores >= tau, so every one of the top KC is >= tau; maxima left
+// out only lower tau.  The candidates (content scores >= tau) are compacted
+// and, when at most kSortCap survive, ranked exactly by all-pairs comparison;
+// otherwise linear-bin radix passes refine the boundary and a bitonic sort
+// orders the survivors.
+template <int NT, int IPT, typename Emit>
+__device__ void select_content(SelectLds<NT>& L, float (&v)[IPT], MaskT<IPT> content, int base, int KC,
+                               int n_max, Emit&& emit) {
+  using Mask = MaskT<IPT>;
+  constexpr Mask kOne = 1;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  {
+    const bool has_max = tid < n_max && L.maxv[tid] != -INFINITY;
+    const uint32_t key = has_max ? (uint32_t)(sel_key(L.maxv[tid], 0) >> 32) : 0u;
+    if (has_max) atomicAdd(&L.rh[key >> 24], 1);
+    __syncthreads();
+    if (w == 0) radix_digit(L.rh, KC, L.bc);          // bc[0] = digit, bc[1] = count above
+    __syncthreads();
+    const uint32_t b1 = (uint32_t)L.bc[0];
+    const int above1 = L.bc[1];
+    if (has_max && (key >> 24) == b1) atomicAdd(&L.rh[256 + ((key >> 16) & 0xffu)], 1);
+    __syncthreads();
+    if (w == 0) {
+      radix_digit(L.rh + 256, KC - above1, L.bc + 2);
+      if (lane == 0) {
+        const uint32_t tk = (b1 << 24) | ((uint32_t)L.bc[2] << 16);
+        const uint32_t u = (tk & 0x80000000u) ? (tk & 0x7fffffffu) : ~tk;
+        L.tau = (above1 < 0 || L.bc[3] < 0) ? -FLT_MAX : fmaxf(__uint_as_float(u), -FLT_MAX);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- candidates: content scores >= tau, one LDS atomic per wave ----
+  const float tau = L.tau;
+  Mask cm = 0;
+  if (tau == -FLT_MAX) {                       // the bottom of the range: compare sanitised scores
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) cm |= (sanitize(v[i]) >= tau) ? (kOne << i) : Mask(0);
+  } else {
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) cm |= (v[i] >= tau) ? (kOne << i) : Mask(0);
+  }
+  cm &= content;
+  {
+    const int c = popcnt(cm);
+    const int inc = wave_incl_scan(c);
+    const int wtot = __builtin_amdgcn_readlane(inc, kWave - 1);
+    if (wtot) {
+      int o0 = 0;
+      if (lane == kWave - 1) o0 = atomicAdd(&L.n, wtot);
+      int o = __builtin_amdgcn_readlane(o0, kWave - 1) + inc - c;
+#pragma unroll
+      for (int i = 0; i < IPT; ++i) {
+        const bool bit = (cm >> i) & kOne;
+        if (__ballot(bit)) {                   // most element positions hold no candidate in the wave
+          if (bit && o < kSortCap) L.keys[o] = sel_key(sanitize(v[i]), base + i);
+          o += bit ? 1 : 0;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int n_cand = L.n;
+  if (n_cand <= kSortCap) {
+    // rank every candidate against all others, the pairs spread over the workgroup
+    if (tid == 0 && (n_cand & 1)) L.keys[n_cand] = 0;   // pad to pairs: key 0 ranks below every key
+    __syncthreads();
+    const int n2 = (n_cand + 1) & ~1;
+    const int npad = next_pow2(max(n_cand, 1));
+    const int parts = max(NT / npad, 1), jlen = (ceil_div(n2, parts) + 1) & ~1;
+    const int i = tid % npad, j0 = (tid / npad) * jlen, j1 = min(n2, j0 + jlen);
+    if (i < n_cand && tid / npad < parts) {
+      const uint64_t ki = L.keys[i];
+      int r = 0;
+#pragma unroll 4
+      for (int j = j0; j < j1; j += 2) {
+        const ulonglong2 y = *reinterpret_cast<const ulonglong2*>(&L.keys[j]);
+        r += (y.x > ki) + (y.y > ki);
+      }
+      if (r) atomicAdd(&L.rank[i], r);
+    }
+    __syncthreads();
+    for (int e = tid; e < n_cand; e += NT)
+      if (L.rank[e] < KC) emit(L.rank[e], key_index(L.keys[e]));
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < IPT; ++i)
+    if ((content >> i) & kOne) v[i] = sanitize(v[i]);
+
+  // ---- fallback: the boundary bin holds too many blocks; refine exactly ----
+  Mask cand = content, sel = 0;
+  int need = KC, nsel = 0;
+  bool sort_union = false;
+  for (;;) {
+    const int cnt = block_reduce<NT>(popcnt(cand), L.i, OpAdd());
+    if (need <= 0) { cand = 0; break; }
+    if (need >= cnt) { sel |= cand; cand = 0; nsel += cnt; need = 0; break; }
+    if (nsel + cnt <= kSortCap) { sort_union = true; break; }
+    if (cnt <= kSortCap) {
+      int tot;
+      const int off = block_excl_scan<NT>(popcnt(cand), L.i, &tot);
+      int o = off;
+#pragma unroll
+      for (int i = 0; i < IPT; ++i)
+        if ((cand >> i) & kOne) L.keys[o++] = sel_key(v[i], base + i);
+      const int n = next_pow2(tot);
+      for (int i = tot + tid; i < n; i += NT) L.keys[i] = 0;
+      __syncthreads();
+      bitonic_desc<NT>(L.keys, n);
+      const uint64_t kth = L.keys[need - 1];
+#pragma unroll
+      for (int i = 0; i < IPT; ++i)
+        if (((cand >> i) & kOne) && sel_key(v[i], base + i) >= kth) sel |= kOne << i;
+      nsel += need; need = 0; cand = 0;
+      __syncthreads();
+      break;
+    }
+    float lo2 = FLT_MAX, hi2 = -FLT_MAX;
+#pragma unroll
+    for (int i = 0; i < IPT; ++i)
+      if ((cand >> i) & kOne) { lo2 = fminf(lo2, v[i]); hi2 = fmaxf(hi2, v[i]); }
+    lo2 = block_reduce<NT>(lo2, L.f, OpMin());
+    hi2 = block_reduce<NT>(hi2, L.f, OpMax());
+    if (lo2 == hi2) {
+      // all candidates tie: take the lowest block indices
+      int tot;
+      const int off = block_excl_scan<NT>(popcnt(cand), L.i, &tot);
+      int r = off;
+#pragma unroll
+      for (int i = 0; i < IPT; ++i)
+        if ((cand >> i) & kOne) { if (r < need) sel |= kOne << i; ++r; }
+      nsel += need; need = 0; cand = 0;
+      break;
+    }
+    // 256 linear bins in double precision: hi2 and lo2 always land in
+    // different bins, so the candidate set shrinks on every pass
+    const double inv = 256.0 / ((double)hi2 - (double)lo2);
+    auto bin2 = [&](float x) { return (int)fmin(255.0, floor(((double)hi2 - (double)x) * inv)); };
+    for (int i = tid; i < 256; i += NT) L.hist[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < IPT; ++i)
+      if ((cand >> i) & kOne) atomicAdd(&L.hist[bin2(v[i])], 1);
+    __syncthreads();
+    if (tid < kWave) {
+      int c4[4], s4 = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { c4[j] = L.hist[4 * tid + j]; s4 += c4[j]; }
+      int before = wave_incl_scan(s4) - s4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (before < need && need <= before + c4[j]) { L.bc[2] = 4 * tid + j; L.bc[3] = before; }
+        before += c4[j];
+      }
+    }
+    __syncthreads();
+    const int bs2 = L.bc[2], above = L.bc[3];
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) {
+      if ((cand >> i) & kOne) {
+        const int bi = bin2(v[i]);
+        if (bi < bs2) { sel |= kOne << i; cand &= ~(kOne << i); }
+        else if (bi > bs2) cand &= ~(kOne << i);
+      }
+    }
+    nsel += above;
+    need -= above;
+    __syncthreads();
+  }
+  const Mask outm = sort_union ? (sel | cand) : sel;
+  int tot;
+  const int off = block_excl_scan<NT>(popcnt(outm), L.i, &tot);
+  if (sort_union || KC <= kSortCap) {
+    int o = off;
+#pragma unroll
+    for (int i = 0; i < IPT; ++i)
+      if ((outm >> i) & kOne) L.keys[o++] = sel_key(v[i], base + i);
+    const int n = next_pow2(tot);
+    for (int i = tot + tid; i < n; i += NT) L.keys[i] = 0;
+    __syncthreads();
+    bitonic_desc<NT>(L.keys, n);
+    for (int j = tid; j < KC; j += NT) emit(j, key_index(L.keys[j]));
+  } else {
+    // more than kSortCap content blocks: listed in block order
+    int o = off;
+#pragma unroll
+    for (int i = 0; i < IPT; ++i)
+      if ((outm >> i) & kOne) emit(o++, base + i);
+  }
+}
+
+}  // namespace adakv
