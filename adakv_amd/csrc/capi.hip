@@ -168,12 +168,11 @@ ScoreArgs score_args(const adakv_geometry_t* g, const adakv_query_t* q, const ad
   return sa;
 }
 
-// Scores (with an optional fused centroid append) and the per-head selection;
-// sel_lens come from the budget kernel when requested, otherwise the decode
-// kernel derives them from the weights left in the workspace.
-int run_plan(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_centroid_t* c,
-             const adakv_kv_t* kv_append, int n_new, const int32_t* lens, const adakv_budget_t* p,
-             int32_t* table, int T, int32_t* sel_lens, char* ws, hipStream_t s) {
+// Scores (with an optional fused centroid append) and their softmax records;
+// returns the selection arguments that consume them.
+int run_scores(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_centroid_t* c,
+               const adakv_kv_t* kv_append, int n_new, const int32_t* lens, const adakv_budget_t* p,
+               int32_t* table, int T, char* ws, hipStream_t s, SelectArgs* se_out) {
   const WorkspaceLayout L = workspace_layout(*g, T);
   ScoreArgs sa = score_args(g, q, c, lens, reinterpret_cast<float*>(ws + L.scores), L.sp);
   if (n_new > 0) {
@@ -185,7 +184,8 @@ int run_plan(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_cent
   sa.parts_pitch = L.parts_pitch;
   sa.cfg = budget_cfg(p);
   if (launch_score(sa, c->dtype, g->head_dim, s) != hipSuccess) return ADAKV_ERR_LAUNCH;
-  SelectArgs se{};
+  SelectArgs& se = *se_out;
+  se = SelectArgs{};
   se.scores = sa.scores; se.sp = L.sp;
   se.seq_lens = lens; se.uniform_len = g->max_seq_len; se.bs = g->block_size;
   se.B = g->batch; se.Hq = g->n_q_heads;
@@ -195,6 +195,18 @@ int run_plan(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_cent
   se.parts = sa.parts; se.parts_pitch = sa.parts_pitch;
   se.n_chunks = sa.n_chunks; se.chunk_rows = sa.chunk_rows;
   se.n_new = n_new;
+  return ADAKV_OK;
+}
+
+// Scores and the per-head selection; sel_lens come from the budget kernel
+// when requested, otherwise the decode kernel derives them from the weights
+// left in the workspace.
+int run_plan(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_centroid_t* c,
+             const adakv_kv_t* kv_append, int n_new, const int32_t* lens, const adakv_budget_t* p,
+             int32_t* table, int T, int32_t* sel_lens, char* ws, hipStream_t s) {
+  SelectArgs se;
+  int st;
+  if ((st = run_scores(g, q, c, kv_append, n_new, lens, p, table, T, ws, s, &se))) return st;
   if (launch_select(se, g->max_blocks, s) != hipSuccess) return ADAKV_ERR_LAUNCH;
   if (!sel_lens) return ADAKV_OK;
   BudgetArgs ba{};
@@ -206,6 +218,32 @@ int run_plan(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_cent
   return status_of(launch_budget(ba, s));
 }
 
+// Decode fields shared by every decode launch: q, K/V, lengths, scale, output.
+DecodeArgs decode_args(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
+                       const int32_t* lens, float sm_scale, const adakv_output_t* out) {
+  DecodeArgs d{};
+  d.q = q->data; d.qdt = q->dtype; d.qsb = q->stride_b; d.qsh = q->stride_h;
+  d.k = kv->k; d.v = kv->v; d.sb = kv->stride_b; d.sh = kv->stride_h; d.ss = kv->stride_s;
+  d.seq_lens = lens; d.uniform_len = g->max_seq_len; d.bs = g->block_size;
+  d.B = g->batch; d.Hq = g->n_q_heads; d.Hkv = g->n_kv_heads; d.G = g->n_q_heads / g->n_kv_heads;
+  d.scale_log2 = sm_scale * 1.4426950408889634f;
+  d.out = out->data; d.odt = out->dtype; d.osb = out->stride_b; d.osh = out->stride_h;
+  return d;
+}
+
+// Largest LDS a workgroup may hold on the current device (cached per device).
+size_t max_lds_per_block() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return kLdsLimit;
+  if (dev < 64 && cache[dev] > 0) return (size_t)cache[dev];
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+    return kLdsLimit;
+  if (dev < 64) cache[dev] = v;
+  return (size_t)v;
+}
+
 // Table-driven sparse decode (table != nullptr) or dense decode (+ merge).
 // With sel_lens == nullptr the per-head counts are derived from the budget
 // weights in the workspace and written to sel_lens_out.
@@ -214,17 +252,11 @@ int run_decode(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv
                const adakv_budget_t* p, int32_t* sel_lens_out, float sm_scale,
                const adakv_output_t* out, char* ws, int T_layout, bool table_unique, hipStream_t s) {
   const WorkspaceLayout L = workspace_layout(*g, T_layout);
-  DecodeArgs d{};
-  d.q = q->data; d.qdt = q->dtype; d.qsb = q->stride_b; d.qsh = q->stride_h;
-  d.k = kv->k; d.v = kv->v; d.sb = kv->stride_b; d.sh = kv->stride_h; d.ss = kv->stride_s;
-  d.seq_lens = lens; d.uniform_len = g->max_seq_len; d.bs = g->block_size;
-  d.B = g->batch; d.Hq = g->n_q_heads; d.Hkv = g->n_kv_heads; d.G = g->n_q_heads / g->n_kv_heads;
+  DecodeArgs d = decode_args(g, q, kv, lens, sm_scale, out);
   d.table = table; d.T = T; d.sel_lens = sel_lens;
   d.wbuf = reinterpret_cast<const double*>(ws + L.weights);
   if (p) d.cfg = budget_cfg(p);
   d.sel_lens_out = sel_lens_out;
-  d.scale_log2 = sm_scale * 1.4426950408889634f;
-  d.out = out->data; d.odt = out->dtype; d.osb = out->stride_b; d.osh = out->stride_h;
   d.partials = reinterpret_cast<float*>(ws + L.partials);
   d.counters = reinterpret_cast<int*>(ws + L.counters_dec);
   d.max_blocks = g->max_blocks;
@@ -404,6 +436,16 @@ int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const 
   int32_t* lens = sel ? sel->sel_lens : reinterpret_cast<int32_t*>(w + L.lens);
   const hipStream_t s = (hipStream_t)stream;
   if (append_new > 0 && !centroid_pair_ok(kv->dtype, c->dtype)) return ADAKV_ERR_DTYPE;
+  // bf16 / fp16 K/V on a shape the fused kernel serves: scores, then one
+  // kernel for the budget, the selection and the decode of every head
+  if (kv->dtype != ADAKV_F32 && select_decode_supported(g->head_dim, g->max_blocks, T) &&
+      select_decode_lds(g->head_dim, g->n_q_heads) <= max_lds_per_block()) {
+    FusedArgs fa{};
+    if ((st = run_scores(g, q, c, kv, append_new, seq_lens, p, table, Tl, w, s, &fa.s))) return st;
+    fa.d = decode_args(g, q, kv, seq_lens, sm_scale, out);
+    fa.d.sel_lens_out = lens;
+    return status_of(launch_select_decode(fa, kv->dtype, g->head_dim, g->max_blocks, s));
+  }
   if ((st = run_plan(g, q, c, kv, append_new, seq_lens, p, table, Tl, nullptr, w, s))) return st;
   // the selection kernel lists distinct valid blocks: no union needed per head
   return run_decode(g, q, kv, seq_lens, table, Tl, nullptr, p, lens, sm_scale, out, w, Tl, true, s);

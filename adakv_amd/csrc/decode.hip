@@ -32,6 +32,7 @@
 // slice to arrive merges them, in dense mode merge_kernel does.
 #include <algorithm>
 
+#include "attend.hpp"
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -40,12 +41,6 @@ namespace {
 
 constexpr int kSparseThreads = 512;
 constexpr int kDenseThreads = 256;
-
-typedef short short4_t __attribute__((ext_vector_type(4)));
-typedef float float4_t __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
 // Prologue: per-head counts and the union list of one (sequence, KV head), and
@@ -571,37 +566,13 @@ __global__ __launch_bounds__(NT) void decode_kernel(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 // Matrix-core streaming kernel (bf16 / fp16 K/V).
 // ---------------------------------------------------------------------------
-template <int KVDT>
-__device__ __forceinline__ float4_t mfma_qk(const uint4& k, const uint4& q, float4_t c) {
-  if constexpr (KVDT == ADAKV_BF16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, k),
-                                                   __builtin_bit_cast(bf16x8_t, q), c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, k),
-                                                  __builtin_bit_cast(f16x8_t, q), c, 0, 0, 0);
-}
-template <int KVDT>
-__device__ __forceinline__ float4_t mfma_pv(const uint2& p, const uint2& v, float4_t c) {
-  if constexpr (KVDT == ADAKV_BF16)
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_t, p),
-                                                     __builtin_bit_cast(short4_t, v), c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, p),
-                                                 __builtin_bit_cast(f16x4_t, v), c, 0, 0, 0);
-}
-template <int KVDT>
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  if constexpr (KVDT == ADAKV_BF16) return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
-  else return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
-}
-
 template <int D, int NT, int GMAX>
 struct MfmaShape {
   static constexpr int NW = NT / kWave;
-  static constexpr int KS = D / 32;            // k-steps of S^T = K . Q^T (16-byte loads per lane)
-  static constexpr int NT16 = D / 16;          // 16-column tiles of O
-  static constexpr int VROW = D / 2 + 2;       // V tile row stride in 4-byte words (conflict-free reads)
-  static constexpr int VT_WORDS = 16 * VROW;
+  static constexpr int KS = TileShape<D>::KS;
+  static constexpr int NT16 = TileShape<D>::NT16;
+  static constexpr int VROW = TileShape<D>::VROW;
+  static constexpr int VT_WORDS = TileShape<D>::VT_WORDS;
   static constexpr int HC0 = 8192 / (NW * D);
   static constexpr int HC = HC0 < 1 ? 1 : (HC0 > GMAX ? GMAX : HC0);   // heads merged per LDS pass
   static constexpr int BIG_WORDS = (NW * VT_WORDS > NW * HC * D) ? NW * VT_WORDS : NW * HC * D;
@@ -627,25 +598,8 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeArgs a) {
   const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
   const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
 
-  // B operand of S^T: lane (col, grp) holds q[head col][D/4*grp + 8*s .. +7] at step s
-  // (the same permutation of head_dim as the K fragments, so the dot products are whole)
   uint4 qf[KS];
-  with_dtype(a.qdt, [&](auto tag) {
-    constexpr int QDT = decltype(tag)::value;
-    const int64_t qo = (int64_t)b * a.qsb + (int64_t)(gr.h0 + min(col, G - 1)) * a.qsh + (D / 4) * grp;
-    float x[KS][8];
-#pragma unroll
-    for (int s = 0; s < KS; ++s)
-#pragma unroll
-      for (int t = 0; t < 8; ++t) x[s][t] = load_t<QDT>(a.q, qo + 8 * s + t);
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      uint32_t wv[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) wv[t] = col < G ? pack2<KVDT>(x[s][2 * t], x[s][2 * t + 1]) : 0u;
-      qf[s] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
-    }
-  });
+  load_q_frag<KVDT, D>(a.q, a.qdt, (int64_t)b * a.qsb + (int64_t)gr.h0 * a.qsh, a.qsh, G, qf);
   const Slice sl = build_slice<NT>(a, b, gr, split, nb, s_dyn_raw, s_cnt, s_misc);
   if (sl.U == 0) {
     if (split == 0) write_nan_outputs(a, b, gr, D, NT);
@@ -662,101 +616,26 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeArgs a) {
   const int n_sub = ceil_div(a.bs, 16);
   const int n_items = (sl.hi - sl.lo) * n_sub;
   uint32_t* vt = s_big + w * S::VT_WORDS;         // this wave's V tile [16 tokens][VROW words]
-  const uint16_t* vt16 = reinterpret_cast<const uint16_t*>(vt);
   const float scale = a.scale_log2;
+  TileState<D> st;
+  tile_init(st);
 
-  float m_h = -INFINITY, l_h = 0.f;               // softmax state of head `col` (l: this lane's tokens)
-  float4_t acc[NT16];                             // O[head 4*grp+i][16*n + col]
-#pragma unroll
-  for (int n = 0; n < NT16; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-  struct Buf { uint4 k[KS], v[KS]; };
   auto item = [&](int j, int& t0, int& t_hi, uint32_t& hm) {
     int blk;
     list_entry(a, gr, s_list, sl.lo, j / n_sub, blk, hm);
     t0 = blk * a.bs + (j % n_sub) * 16;
     t_hi = min(min(blk * a.bs + a.bs, len), t0 + 16);
   };
-  // Tokens past the tile's end load the tile's last row instead (always in
-  // bounds, so the loads need no predication); their weights are zeroed.
-  auto load = [&](int t0, int t_hi, Buf& r) {
-    const int64_t o = (int64_t)min(t0 + col, t_hi - 1) * row_bytes;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      r.k[s] = load16(kbase + o + 16 * s);
-      r.v[s] = load16(vbase + o + 16 * s);
-    }
+  auto load = [&](int t0, int t_hi, TileBuf<D>& r) { tile_load<D>(kbase, vbase, row_bytes, t0, t_hi, r); };
+  auto compute = [&](int t0, int t_hi, uint32_t hm, const TileBuf<D>& r) {
+    tile_update<KVDT, D>(st, r, qf, vt, t0, t_hi, col < G && ((hm >> col) & 1u), scale);
   };
-  auto compute = [&](int t0, int t_hi, uint32_t hm, const Buf& r) {
-    // V rows to this wave's LDS tile for the transposed B-operand reads; the
-    // previous tile's reads were issued before these writes (LDS operations of
-    // a wave complete in order), the compiler barriers keep that order.
-    __asm__ volatile("" ::: "memory");
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      uint32_t* p = vt + col * VROW + (D / 8) * grp + 4 * s;
-      *reinterpret_cast<uint2*>(p) = make_uint2(r.v[s].x, r.v[s].y);
-      *reinterpret_cast<uint2*>(p + 2) = make_uint2(r.v[s].z, r.v[s].w);
-    }
-    __asm__ volatile("" ::: "memory");
-    // S^T[token 4*grp+i][head col]
-    float4_t sc = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KS; ++s) sc = mfma_qk<KVDT>(r.k[s], qf[s], sc);
-    const bool head_on = col < G && ((hm >> col) & 1u);
-    float sv[4];
-    float mt = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool ok = head_on && (t0 + 4 * grp + i < t_hi);
-      sv[i] = ok ? sc[i] * scale : -INFINITY;
-      mt = fmaxf(mt, sv[i]);
-    }
-    LanePair pr = swap16(mt);
-    mt = fmaxf(pr.a, pr.b);
-    pr = swap32(mt);
-    mt = fmaxf(pr.a, pr.b);
-    const float mn = fmaxf(m_h, mt);
-    const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_h - mn);
-    float ps = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sv[i] = sv[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[i] - mn);
-      ps += sv[i];
-    }
-    l_h = l_h * alpha + ps;
-    m_h = mn;
-    // rescale the O rows (heads 4*grp+i) by their heads' alpha, held by lanes col == head
-    float al[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      al[i] = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * grp + i) * 4, __float_as_int(alpha)));
-#pragma unroll
-    for (int n = 0; n < NT16; ++n)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[n][i] *= al[i];
-    // O += P . V: A = P[head col][tokens 4*grp .. +3] (the S^T layout), B = V[tokens][16 dims]
-    const uint2 pf = make_uint2(pack2<KVDT>(sv[0], sv[1]), pack2<KVDT>(sv[2], sv[3]));
-#pragma unroll
-    for (int n = 0; n < NT16; ++n) {
-      const int c16 = n * 16 + col;
-      const uint32_t v0 = vt16[(4 * grp + 0) * 2 * VROW + c16], v1 = vt16[(4 * grp + 1) * 2 * VROW + c16];
-      const uint32_t v2 = vt16[(4 * grp + 2) * 2 * VROW + c16], v3 = vt16[(4 * grp + 3) * 2 * VROW + c16];
-      acc[n] = mfma_pv<KVDT>(pf, make_uint2(v0 | (v1 << 16), v2 | (v3 << 16)), acc[n]);
-    }
-  };
-  stream_items<NW, Buf>(w, n_items, item, load, compute);
+  stream_items<NW, TileBuf<D>>(w, n_items, item, load, compute);
 
-  // denominator of head col over the wave's 4 lane groups
-  {
-    LanePair pr = swap16(l_h);
-    l_h = pr.a + pr.b;
-    pr = swap32(l_h);
-    l_h = pr.a + pr.b;
-  }
+  tile_finish(st);
   if (grp == 0 && col < G) {
-    s_m[w][col] = m_h;
-    s_l[w][col] = l_h;
+    s_m[w][col] = st.m_h;
+    s_l[w][col] = st.l_h;
   }
   __syncthreads();                                  // the V tiles are dead: s_big becomes s_acc
   auto s_acc = reinterpret_cast<float (*)[HC][D]>(s_big);
@@ -766,7 +645,7 @@ __global__ __launch_bounds__(NT) void decode_mfma_kernel(DecodeArgs a) {
       const int head = 4 * grp + i;
       if (head >= g0 && head < g0 + n)
 #pragma unroll
-        for (int t = 0; t < NT16; ++t) s_acc[w][head - g0][t * 16 + col] = acc[t][i];
+        for (int t = 0; t < NT16; ++t) s_acc[w][head - g0][t * 16 + col] = st.acc[t][i];
     }
   });
 }

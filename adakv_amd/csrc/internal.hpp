@@ -37,17 +37,18 @@ struct ScoreArgs {
   const void* k;
   int kdt;
   int64_t ksb, ksh, kss;
-  // per-chunk softmax partials of the scores (nullptr: not wanted), one
-  // PartRecord per (sequence, q-head, chunk) at parts[(b * Hq + h) * parts_pitch + chunk]
+  // softmax records of the scores (nullptr: not wanted), one per (sequence,
+  // q-head, score workgroup) at parts[((b * Hq + h) * parts_pitch + unit) * kPartFloats]
   float* parts;
   int parts_pitch;
   BudgetCfg cfg;
   int n_app, n_chunks, chunk_rows;   // set by the launcher
 };
 
-// Softmax partial of one chunk of a head's scores z = score / temperature:
-// m = max z, S = sum exp(z - m), T = sum exp(z - m) * (z - m), and the range
-// [lo, hi] of the chunk's sanitised content scores.  8 floats (32 bytes).
+// Softmax record of a score workgroup's rows for one head (z = score /
+// temperature): m = max z, S = sum exp(z - m), T = sum exp(z - m) * (z - m),
+// then the sanitised content maxima of its 4 sub-chunks (-inf: none) and one
+// unused float.  8 floats (32 bytes).
 constexpr int kPartFloats = 8;
 
 struct SelectArgs {
@@ -60,8 +61,8 @@ struct SelectArgs {
   int32_t* table;              // [B, Hq, T]
   int T;
   double* wbuf;                // [B, Hq] entropy weights (adaptive policy)
-  const float* parts;          // per-chunk partials written by the score kernel
-  int parts_pitch, n_chunks, chunk_rows;
+  const float* parts;          // softmax records written by the score kernel
+  int parts_pitch, n_chunks, chunk_rows;   // records per (sequence, head) row, rows per record
   int n_new;                   // rows >= first appended block are not in any chunk partial
 };
 
@@ -105,6 +106,14 @@ struct DecodeArgs {
   int table_unique;            // 1: the first sel_lens entries of a row are distinct valid blocks
 };
 
+// Fused selection + sparse decode (bf16 / fp16 K/V): the selection fields
+// (scores, records, budget, table) and the decode fields (q, K/V, output,
+// sel_lens_out) of one step.
+struct FusedArgs {
+  SelectArgs s;
+  DecodeArgs d;
+};
+
 struct MergeArgs {
   const float* partials;
   int nsplit;
@@ -138,5 +147,10 @@ hipError_t launch_decode(const DecodeArgs& a, int kvdt, int D, hipStream_t s);
 int decode_threads(int kvdt, int D, bool sparse);
 size_t decode_static_lds(int kvdt, int D, int gmax, bool sparse);
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
+// Fused selection + decode: whether it serves a shape, its LDS bytes (static
+// + dynamic) for a head_dim and q-head count, and the launcher.
+bool select_decode_supported(int D, int max_blocks, int table_width);
+size_t select_decode_lds(int D, int Hq);
+hipError_t launch_select_decode(const FusedArgs& a, int kvdt, int D, int max_blocks, hipStream_t s);
 
 }  // namespace adakv

@@ -90,17 +90,17 @@ __device__ __forceinline__ SoftPart soft_merge(const SoftPart& x, const SoftPart
                   (x.m == -INFINITY ? 0.f : fx * fmaf(dx, x.S, x.T)) + (y.m == -INFINITY ? 0.f : fy * fmaf(dy, y.S, y.T))};
 }
 
-// Merge over aligned groups of N lanes (N = 32 or 64): the max first, then
-// every lane rescales its sums to it once and the sums are added.
+// Merge over aligned groups of N lanes (N = 16, 32 or 64): the max first,
+// then every lane rescales its sums to it once and the sums are added.
 template <int N>
 __device__ __forceinline__ SoftPart soft_group_merge(SoftPart p) {
-  static_assert(N == 32 || N == 64, "half-wave or wave groups");
+  static_assert(N == 16 || N == 32 || N == 64, "row, half-wave or wave groups");
   float M = p.m;
   M = fmaxf(M, dpp_mov<0xB1>(M));
   M = fmaxf(M, dpp_mov<0x4E>(M));
   M = fmaxf(M, dpp_mov<0x141>(M));
   M = fmaxf(M, dpp_mov<0x140>(M));
-  { const LanePair q = swap16(M); M = fmaxf(q.a, q.b); }
+  if constexpr (N >= 32) { const LanePair q = swap16(M); M = fmaxf(q.a, q.b); }
   if constexpr (N == 64) { const LanePair q = swap32(M); M = fmaxf(q.a, q.b); }
   float S = 0.f, T = 0.f;
   if (p.m != -INFINITY) {
