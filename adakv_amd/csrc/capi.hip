@@ -194,6 +194,8 @@ int run_scores(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_ce
   se.wbuf = reinterpret_cast<double*>(ws + L.weights);
   se.parts = sa.parts; se.parts_pitch = sa.parts_pitch;
   se.n_chunks = sa.n_chunks; se.chunk_rows = sa.chunk_rows;
+  se.chunk_shift = __builtin_ctz((unsigned)sa.chunk_rows);
+  se.bs_shift = (g->block_size & (g->block_size - 1)) == 0 ? __builtin_ctz((unsigned)g->block_size) : -1;
   se.n_new = n_new;
   return ADAKV_OK;
 }
@@ -436,9 +438,11 @@ int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const 
   int32_t* lens = sel ? sel->sel_lens : reinterpret_cast<int32_t*>(w + L.lens);
   const hipStream_t s = (hipStream_t)stream;
   if (append_new > 0 && !centroid_pair_ok(kv->dtype, c->dtype)) return ADAKV_ERR_DTYPE;
-  // bf16 / fp16 K/V on a shape the fused kernel serves: scores, then one
-  // kernel for the budget, the selection and the decode of every head
-  if (kv->dtype != ADAKV_F32 && select_decode_supported(g->head_dim, g->max_blocks, T) &&
+  // bf16 / fp16 K/V (and q of the same type) on a shape the fused kernel
+  // serves: scores, then one kernel for the budget, the selection and the
+  // decode of every head
+  if (kv->dtype != ADAKV_F32 && q->dtype == kv->dtype &&
+      select_decode_supported(g->head_dim, g->max_blocks, T, g->n_q_heads, L.sp, L.parts_pitch) &&
       select_decode_lds(g->head_dim, g->n_q_heads) <= max_lds_per_block()) {
     FusedArgs fa{};
     if ((st = run_scores(g, q, c, kv, append_new, seq_lens, p, table, Tl, w, s, &fa.s))) return st;

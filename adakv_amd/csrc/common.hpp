@@ -315,23 +315,24 @@ __device__ __forceinline__ int head_count(const Bounds& r, int policy, double w,
 // NumPy's pairwise summation of a contiguous fp64 array (8 accumulators for
 // blocks of <= 128 elements, halving above), so that the device reproduces
 // w.sum() of adakv/budget.py:84 bit for bit.
-template <int DEPTH>
-__device__ double numpy_pairwise_sum(const double* a, int n) {
+__device__ __forceinline__ double pairwise_block(const double* a, int n) {   // n <= 128
   if (n < 8) {
     double r = 0.0;
     for (int i = 0; i < n; ++i) r += a[i];
     return r;
   }
-  if (n <= 128 || DEPTH == 0) {
-    double r[8];
-    for (int j = 0; j < 8; ++j) r[j] = a[j];
-    int i = 8;
-    for (; i < n - (n % 8); i += 8)
-      for (int j = 0; j < 8; ++j) r[j] += a[i + j];
-    double res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
-    for (; i < n; ++i) res += a[i];
-    return res;
-  }
+  double r[8];
+  for (int j = 0; j < 8; ++j) r[j] = a[j];
+  int i = 8;
+  for (; i < n - (n % 8); i += 8)
+    for (int j = 0; j < 8; ++j) r[j] += a[i + j];
+  double res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+  for (; i < n; ++i) res += a[i];
+  return res;
+}
+template <int DEPTH>
+__device__ double numpy_pairwise_sum(const double* a, int n) {
+  if (n <= 128 || DEPTH == 0) return pairwise_block(a, n);
   int n2 = n / 2;
   n2 -= n2 % 8;
   if constexpr (DEPTH > 0)

@@ -35,6 +35,7 @@ namespace {
 
 constexpr int kFusedThreads = 512;
 constexpr int kLanesPerHead = 16;            // lanes merging one head's records
+constexpr int kRecsPerLane = 4;              // records a lane loads up front
 
 // Decode waves: all 8.
 template <int D>
@@ -52,11 +53,47 @@ constexpr size_t fused_static_lds() {
   return sizeof(FusedBig<D>) + kSortCap * sizeof(int) + 2 * fused_decode_waves<D>() * sizeof(float);
 }
 
+// x / d, with s = log2(d) when d is a power of two (else -1).
+__device__ __forceinline__ int div_p2(int x, int d, int s) { return s >= 0 ? (x >> s) : x / d; }
+
+__device__ __forceinline__ double readlane_d(double x, int l) {
+  const long long u = __double_as_longlong(x);
+  const int lo = __builtin_amdgcn_readlane((int)(u & 0xffffffffll), l);
+  const int hi = __builtin_amdgcn_readlane((int)(u >> 32), l);
+  return __longlong_as_double(((long long)hi << 32) | (uint32_t)lo);
+}
+
+// NumPy's pairwise sum of a[0, n) for n <= 128 (the single-block case of
+// numpy_pairwise_sum), by one wave: lane j < 8 is NumPy's accumulator j
+// (a[j] + a[j + 8] + ... in order), then the fixed combination and the tail.
+// Every lane receives the sum.
+__device__ __forceinline__ double wave_pairwise_sum(const double* a, int n) {
+  if (n < 8) {
+    double r = 0.0;
+    for (int i = 0; i < n; ++i) r += a[i];
+    return r;
+  }
+  const int lane = threadIdx.x & (kWave - 1);
+  const int m8 = n - (n % 8);
+  double r = 0.0;
+  if (lane < 8) {
+    r = a[lane];
+    for (int i = 8 + lane; i < m8; i += 8) r += a[i];
+  }
+  double x[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) x[j] = readlane_d(r, j);
+  double res = ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
+  for (int i = m8; i < n; ++i) res += a[i];
+  return res;
+}
+
 template <int KVDT, int D, int IPT>
 __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs fa) {
   constexpr int NT = kFusedThreads, NW = NT / kWave;
   constexpr int DW = fused_decode_waves<D>();
   constexpr int NT16 = TileShape<D>::NT16;
+  constexpr int LPH = kLanesPerHead, HPW = kWave / LPH, RPL = kRecsPerLane;
   using Mask = MaskT<IPT>;
   constexpr Mask kOne = 1;
   __shared__ __align__(16) FusedBig<D> big;
@@ -71,7 +108,7 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
   const int col = lane & 15, grp = lane >> 4;
   const int Hq = a.Hq;
   const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
-  const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
+  const int nb = len > 0 ? div_p2(len + a.bs - 1, a.bs, a.bs_shift) : 0;
   const Bounds bb = budget_bounds(nb, a.cfg);
   const int nf = bb.n_forced;
   const int c_lo = bb.sink, c_hi = nb - bb.local;
@@ -88,57 +125,77 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
   select_init(big.sel);
 
   // ---- 1. loads ----
-  // (a) the first record of each 16-lane row's head: all heads when the
-  //     budget is adaptive (four per wave and pass), else only this head (for
-  //     its content maxima).  Records j < n_ck come from the score workgroups,
-  //     j >= n_ck are the rows no record covers (the decode-time append).
-  const int first_app = a.n_new > 0 ? max(len - a.n_new, 0) / a.bs : nb;
+  // Every load here is unconditional, its index clamped in bounds (values not
+  // wanted are discarded where they are consumed): a load under a branch makes
+  // the compiler wait for it where the branches join.
+  //
+  // (a) the records of each 16-lane row's head (RPL per lane, the rest later
+  //     if a head has more): all heads when the budget is adaptive (four per
+  //     wave and pass), else only this head (for its content maxima), and the
+  //     score of one row no record covers (the decode-time append).
+  const int first_app = a.n_new > 0 ? div_p2(max(len - a.n_new, 0), a.bs, a.bs_shift) : nb;
   const int rows_in_chunks = min(nb, first_app);
-  const int n_ck = ceil_div(rows_in_chunks, a.chunk_rows);
-  const int n_virt = n_ck + (nb - rows_in_chunks);
+  const int n_ck = (rows_in_chunks + a.chunk_rows - 1) >> a.chunk_shift;   // records
+  const int n_extra = nb - rows_in_chunks;                                 // rows no record covers
   const float tf = (float)fmax(a.cfg.temperature, 1e-6);
-  constexpr int LPH = kLanesPerHead, HPW = kWave / LPH;
   const int hl = lane % LPH;
   auto head_of = [&](int p) -> int {
     if (adaptive) return (p * NW + w) * HPW + lane / LPH;
     return (w == 0 && lane < LPH) ? h : -1;
   };
-  auto fetch = [&](int hh, int j, float4& r0, float4& r1) {
-    if (j < n_ck) {
-      const float4* rec = reinterpret_cast<const float4*>(
-          a.parts + (((int64_t)b * Hq + hh) * a.parts_pitch + j) * kPartFloats);
-      r0 = rec[0];
-      r1 = rec[1];
-    } else {
-      r0.x = a.scores[((int64_t)b * Hq + hh) * a.sp + rows_in_chunks + (j - n_ck)];
-    }
+  // per-lane offsets stay 32-bit (the host bounds Hq * pitch)
+  const float* parts_b = a.parts + (int64_t)b * Hq * a.parts_pitch * kPartFloats;
+  const float* scores_b = a.scores + (int64_t)b * Hq * a.sp;
+  auto rec = [&](int hh, int j) {
+    return reinterpret_cast<const float4*>(parts_b + (hh * a.parts_pitch + min(j, max(n_ck - 1, 0))) * kPartFloats);
   };
+  auto extra = [&](int hh, int e) { return scores_b + hh * a.sp + min(rows_in_chunks + e, nb - 1); };
   const int hh0 = head_of(0);
-  const bool on0 = hh0 >= 0 && hh0 < Hq && hl < n_virt;
-  float4 r0 = make_float4(0.f, 0.f, 0.f, 0.f), r1 = r0;
-  if (on0) fetch(hh0, hl, r0, r1);
+  const int hs0 = (hh0 >= 0 && hh0 < Hq) ? hh0 : h;
+  float4 R0[RPL], R1[RPL];
+#pragma unroll
+  for (int u = 0; u < RPL; ++u) {
+    R0[u] = rec(hs0, hl + LPH * u)[0];
+    R1[u] = rec(hs0, hl + LPH * u)[1];
+  }
+  const float X0 = *extra(hs0, hl);
   __builtin_amdgcn_sched_barrier(0);
-  // (b) this head's scores: thread t owns blocks [t*IPT, (t+1)*IPT)
+  // (b) this head's scores: thread t owns blocks [t*IPT, (t+1)*IPT); rows
+  //     past nb (stale) are never content
   float v[IPT];
-  load_scores(a.scores + ((int64_t)b * Hq + h) * a.sp, nb, v);
+  {
+    const float* srow = scores_b + h * a.sp;
+#pragma unroll
+    for (int i = 0; i < IPT; i += 4) {
+      const float4 f = *reinterpret_cast<const float4*>(srow + min(tid * IPT + i, a.sp - 4));
+      v[i] = f.x; v[i + 1] = f.y; v[i + 2] = f.z; v[i + 3] = f.w;
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
-  // (c) the query (B operand, head in column 0)
-  uint4 qf[D / 32];
-  load_q_frag<KVDT, D>(d.q, d.qdt, (int64_t)b * d.qsb + (int64_t)h * d.qsh, d.qsh, 1, qf);
+  // (c) the query (same 16-bit type as K), raw until the decode: lane (col,
+  //     grp) holds q[D/4*grp + 8*s + t]
+  uint32_t qraw[D / 32][8];
+  {
+    const uint16_t* qp = reinterpret_cast<const uint16_t*>(d.q) + (int64_t)b * d.qsb + (int64_t)h * d.qsh + (D / 4) * grp;
+#pragma unroll
+    for (int s2 = 0; s2 < D / 32; ++s2)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) qraw[s2][t] = qp[8 * s2 + t];
+  }
   __builtin_amdgcn_sched_barrier(0);
   // (d) the forced tiles: item i (16-token sub-tile i % n_sub of list entry
   //     i / n_sub) belongs to decode wave i % DW; the first n_forced entries
   //     are the sink blocks then the local blocks, as in the table row
-  const int n_sub = ceil_div(a.bs, 16);
+  const int n_sub = (a.bs + 15) >> 4;
   const int nf_items = nf * n_sub;
   const int64_t head_off = ((int64_t)b * d.sb + (int64_t)(h / d.G) * d.sh + (D / 4) * grp) * 2;
   const char* kbase = reinterpret_cast<const char*>(d.k) + head_off;
   const char* vbase = reinterpret_cast<const char*>(d.v) + head_off;
   const int64_t row_bytes = d.ss * 2;
   auto item = [&](int j, int& t0, int& t_hi) {
-    const int e = j / n_sub;
+    const int e = n_sub == 1 ? j : j / n_sub, sub = j - e * n_sub;
     const int blk = e < bb.sink ? e : (e < nf ? local_lo + (e - bb.sink) : s_list[e - nf]);
-    t0 = blk * a.bs + (j % n_sub) * 16;
+    t0 = blk * a.bs + sub * 16;
     t_hi = min(min(blk * a.bs + a.bs, len), t0 + 16);
   };
   const bool pre = w < DW && w < nf_items;   // uniform over the wave
@@ -149,51 +206,58 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
     tile_load<D>(kbase, vbase, row_bytes, p0, p1, P);
   }
   __builtin_amdgcn_sched_barrier(0);
+  const double lognb = log((double)max(nb, 2));   // while the loads are in flight
 
   // ---- 2. entropy weights and this head's content maxima ----
-  auto consume = [&](int hh, int j, const float4& q0, const float4& q1, SoftPart& pt) {
-    SoftPart x;
-    if (j < n_ck) {
-      x = SoftPart{q0.x, q0.y, q0.z};
-      if (hh == h) {
-        const float mx[4] = {q0.w, q1.x, q1.y, q1.z};
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (4 * j + i < NT) big.sel.maxv[4 * j + i] = mx[i];
-      }
-    } else {
-      const int r = rows_in_chunks + (j - n_ck);
-      x = SoftPart{tf == 1.f ? q0.x : __fdiv_rn(q0.x, tf), 1.f, 0.f};
-      const int t = 4 * n_ck + (j - n_ck);
-      if (hh == h && t < NT) big.sel.maxv[t] = (r >= c_lo && r < c_hi) ? sanitize(q0.x) : -INFINITY;
-    }
-    pt = soft_merge(pt, x);
-  };
+  // Maxima of record j at 4j .. 4j+3, of row e no record covers at 4*n_ck + e.
   const int passes = adaptive ? ceil_div(Hq, HPW * NW) : 1;
   for (int p = 0; p < passes; ++p) {
     const int hh = head_of(p);
     const bool on = hh >= 0 && hh < Hq;
-    SoftPart pt = soft_empty();
+    const int hs = on ? hh : h;
+    float4 Q0[RPL], Q1[RPL];
+    float X;
     if (p == 0) {
-      if (on0) consume(hh, hl, r0, r1, pt);
-    } else if (on && hl < n_virt) {
-      float4 q0, q1;
-      fetch(hh, hl, q0, q1);
-      consume(hh, hl, q0, q1, pt);
+#pragma unroll
+      for (int u = 0; u < RPL; ++u) { Q0[u] = R0[u]; Q1[u] = R1[u]; }
+      X = X0;
+    } else {
+#pragma unroll
+      for (int u = 0; u < RPL; ++u) { Q0[u] = rec(hs, hl + LPH * u)[0]; Q1[u] = rec(hs, hl + LPH * u)[1]; }
+      X = *extra(hs, hl);
     }
-    for (int j = hl + LPH; on && j < n_virt; j += LPH) {   // heads with more records than lanes
-      float4 q0, q1;
-      fetch(hh, j, q0, q1);
-      consume(hh, j, q0, q1, pt);
+    SoftPart pt = soft_empty();
+    if (on) {
+      const bool own = hh == h;
+      auto take_rec = [&](int j, const float4& q0, const float4& q1) {
+        pt = soft_merge(pt, SoftPart{q0.x, q0.y, q0.z});
+        if (own) {
+          const float mx[4] = {q0.w, q1.x, q1.y, q1.z};
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (4 * j + i < NT) big.sel.maxv[4 * j + i] = mx[i];
+        }
+      };
+      auto take_row = [&](int e, float x) {
+        pt = soft_merge(pt, SoftPart{tf == 1.f ? x : __fdiv_rn(x, tf), 1.f, 0.f});
+        const int r = rows_in_chunks + e, t = 4 * n_ck + e;
+        if (own && t < NT) big.sel.maxv[t] = (r >= c_lo && r < c_hi) ? sanitize(x) : -INFINITY;
+      };
+#pragma unroll
+      for (int u = 0; u < RPL; ++u)
+        if (hl + LPH * u < n_ck) take_rec(hl + LPH * u, Q0[u], Q1[u]);
+      for (int j = hl + LPH * RPL; j < n_ck; j += LPH) take_rec(j, rec(hh, j)[0], rec(hh, j)[1]);   // long heads
+      if (hl < n_extra) take_row(hl, X);
+      for (int e = hl + LPH; e < n_extra; e += LPH) take_row(e, *extra(hh, e));
     }
     pt = soft_group_merge<LPH>(pt);
-    if (adaptive && on && hl == 0) s_w[hh] = entropy_weight(pt, nb);
+    if (adaptive && on && hl == 0) s_w[hh] = entropy_weight(pt, lognb);
   }
   __syncthreads();
 
   // ---- 3. the head's count and selection ----
-  // every thread evaluates the sum of weights in NumPy's order (LDS broadcasts)
-  const double wsum = adaptive ? numpy_pairwise_sum<6>(s_w, Hq) : 0.0;
+  // every wave evaluates the sum of weights in NumPy's order
+  const double wsum = !adaptive ? 0.0 : Hq <= 128 ? wave_pairwise_sum(s_w, Hq) : numpy_pairwise_sum<6>(s_w, Hq);
   const int k = min(head_count(bb, a.cfg.policy, adaptive ? s_w[h] : 0.0, wsum, Hq), a.T);
   if (tid == 0) {
     if (d.sel_lens_out) d.sel_lens_out[(int64_t)b * Hq + h] = k;
@@ -203,13 +267,14 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
   for (int j = tid; j < nf; j += NT) trow[j] = j < bb.sink ? j : local_lo + (j - bb.sink);
   for (int j = k + tid; j < a.T; j += NT) trow[j] = -1;
   if (KC > 0) {
+    if (w == 0) select_threshold(big.sel, KC, min(4 * n_ck + n_extra, NT));
+    __syncthreads();
     const int base = tid * IPT;
     Mask content = 0;
 #pragma unroll
     for (int i = 0; i < IPT; ++i)
       if (base + i >= c_lo && base + i < c_hi) content |= kOne << i;
-    const int n_max = min(4 * n_ck + (nb - rows_in_chunks), NT);
-    select_content<NT, IPT>(big.sel, v, content, base, KC, n_max, [&](int r, int blk) {
+    select_content<NT, IPT>(big.sel, v, content, base, KC, [&](int r, int blk) {
       s_list[r] = blk;
       trow[nf + r] = blk;
     });
@@ -221,6 +286,15 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
   tile_init(st);
   const int n_items = k * n_sub;
   if (w < DW) {
+    // B operand of S^T: the head in column 0, the other columns zero
+    uint4 qf[D / 32];
+#pragma unroll
+    for (int s2 = 0; s2 < D / 32; ++s2) {
+      uint32_t wv[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) wv[t] = col == 0 ? (qraw[s2][2 * t] | (qraw[s2][2 * t + 1] << 16)) : 0u;
+      qf[s2] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+    }
     uint32_t* vt = big.vt + w * TileShape<D>::VT_WORDS;
     const float scale = d.scale_log2;
     auto load = [&](int t0, int t_hi, TileBuf<D>& r) { tile_load<D>(kbase, vbase, row_bytes, t0, t_hi, r); };
@@ -335,8 +409,9 @@ hipError_t launch_fk(const FusedArgs& a, int D, int max_blocks, hipStream_t s) {
 // The fused kernel serves head_dim <= 128 and up to 16 scores per thread (the
 // register budget of a 512-thread workgroup); other shapes take the
 // three-kernel path.
-bool select_decode_supported(int D, int max_blocks, int table_width) {
-  return D <= 128 && max_blocks <= kFusedThreads * 16 && table_width <= kSortCap;
+bool select_decode_supported(int D, int max_blocks, int table_width, int Hq, int sp, int parts_pitch) {
+  return D <= 128 && max_blocks <= kFusedThreads * 16 && table_width <= kSortCap &&
+         (int64_t)Hq * sp < (1ll << 31) && (int64_t)Hq * parts_pitch * kPartFloats < (1ll << 31);
 }
 
 size_t select_decode_lds(int D, int Hq) {

@@ -63,6 +63,8 @@ struct SelectArgs {
   double* wbuf;                // [B, Hq] entropy weights (adaptive policy)
   const float* parts;          // softmax records written by the score kernel
   int parts_pitch, n_chunks, chunk_rows;   // records per (sequence, head) row, rows per record
+  int chunk_shift;             // log2(chunk_rows) (a power of two)
+  int bs_shift;                // log2(bs) when bs is a power of two, else -1
   int n_new;                   // rows >= first appended block are not in any chunk partial
 };
 
@@ -149,7 +151,7 @@ size_t decode_static_lds(int kvdt, int D, int gmax, bool sparse);
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 // Fused selection + decode: whether it serves a shape, its LDS bytes (static
 // + dynamic) for a head_dim and q-head count, and the launcher.
-bool select_decode_supported(int D, int max_blocks, int table_width);
+bool select_decode_supported(int D, int max_blocks, int table_width, int Hq, int sp, int parts_pitch);
 size_t select_decode_lds(int D, int Hq);
 hipError_t launch_select_decode(const FusedArgs& a, int kvdt, int D, int max_blocks, hipStream_t s);
 

@@ -234,26 +234,28 @@ __device__ void score_chunk_mfma(const ScoreArgs& a, int b, int kvh, int unit, i
   const bool wave_on = wrow0 < nrows;       // uniform over the wave
   float m = -INFINITY, S = 0.f, T = 0.f, hi = -INFINITY;
   if (wave_on) {
-    // A fragments: lane (col, grp) reads row wrow0 + 16t + col, elements [D/4*grp, D/4*(grp+1))
+    // A fragments: lane (col, grp) reads row wrow0 + 16t + col, elements
+    // [32s + 8grp, 32s + 8grp + 8) at k-step s, so that the 4 lanes of a row
+    // read one whole 64-byte segment per load instruction
     const char* cbase = reinterpret_cast<const char*>(a.c) +
-                        ((((int64_t)b * a.Hkv + kvh) * a.max_blocks) * D + (D / 4) * grp) * 2;
+                        ((((int64_t)b * a.Hkv + kvh) * a.max_blocks) * D + 8 * grp) * 2;
     uint4 cf[TPW][KS];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       const int r = min(wrow0 + 16 * t + col, nrows - 1);     // in bounds; extra rows masked below
 #pragma unroll
-      for (int s = 0; s < KS; ++s) cf[t][s] = load16(cbase + (int64_t)r * D * 2 + 16 * s);
+      for (int s = 0; s < KS; ++s) cf[t][s] = load16(cbase + (int64_t)r * D * 2 + 64 * s);
     }
-    // B fragments: lane (col, grp) holds q[head col][D/4*grp + 8s .. +7]
+    // B fragments: lane (col, grp) holds q[head col][32s + 8grp .. +7]
     uint4 qf[KS];
     with_dtype(a.qdt, [&](auto tag) {
       constexpr int QDT = decltype(tag)::value;
-      const int64_t qo = (int64_t)b * a.qsb + (int64_t)(kvh * G + min(col, G - 1)) * a.qsh + (D / 4) * grp;
+      const int64_t qo = (int64_t)b * a.qsb + (int64_t)(kvh * G + min(col, G - 1)) * a.qsh + 8 * grp;
       float x[KS][8];
 #pragma unroll
       for (int s = 0; s < KS; ++s)
 #pragma unroll
-        for (int u = 0; u < 8; ++u) x[s][u] = load_t<QDT>(a.q, qo + 8 * s + u);
+        for (int u = 0; u < 8; ++u) x[s][u] = load_t<QDT>(a.q, qo + 32 * s + u);
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         uint32_t wv[4];
@@ -479,13 +481,15 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
 
   if (KC > 0) {
     const int nf = bb.n_forced;
-    select_content<NT, IPT>(L, v, content, base, KC, n_max, [&](int r, int blk) { trow[nf + r] = blk; });
+    if (w == 0) select_threshold(L, KC, n_max);
+    __syncthreads();
+    select_content<NT, IPT>(L, v, content, base, KC, [&](int r, int blk) { trow[nf + r] = blk; });
   }
   // the head's entropy weight from the waves' partials (adakv/budget.py:33-37)
   if (adaptive && w == NW - 1) {
     SoftPart p = lane < NW ? SoftPart{s_r[lane][0], s_r[lane][1], s_r[lane][2]} : soft_empty();
     p = soft_group_merge<kWave>(p);
-    if (lane == 0) a.wbuf[(int64_t)b * a.Hq + h] = entropy_weight(p, nb);
+    if (lane == 0) a.wbuf[(int64_t)b * a.Hq + h] = entropy_weight(p, log((double)max(nb, 2)));
   }
 }
 

@@ -113,10 +113,10 @@ __device__ __forceinline__ SoftPart soft_group_merge(SoftPart p) {
 
 // Normalised entropy weight (adakv/budget.py:33-37) from the merged partial of
 // all of a head's scores: -sum p log p / log(max(nb, 2)) + 1e-6, in fp64 after
-// the division as NumPy promotes it.
-__device__ __forceinline__ double entropy_weight(const SoftPart& p, int nb) {
+// the division as NumPy promotes it; lognb = log((double)max(nb, 2)).
+__device__ __forceinline__ double entropy_weight(const SoftPart& p, double lognb) {
   const float hs = p.T / p.S - __logf(p.S);
-  return (double)(-hs) / log((double)max(nb, 2)) + 1e-6;
+  return (double)(-hs) / lognb + 1e-6;
 }
 
 // ---- the selection ---------------------------------------------------------
@@ -134,7 +134,7 @@ struct SelectLds {
   int n;
 };
 
-// Clears what select_content expects to start at zero; before the first barrier.
+// Clears what the selection expects to start at zero; before the first barrier.
 template <int NT>
 __device__ __forceinline__ void select_init(SelectLds<NT>& L) {
   const int tid = threadIdx.x;
@@ -178,52 +178,58 @@ __device__ __forceinline__ void radix_digit(const int* hist, int need, int* out)
   if (lane == 0 && (tot < need || need <= 0)) { out[0] = 0; out[1] = -1; }
 }
 
-// The KC largest content scores of a head, by (score desc, block asc), with
-// NaN ranked last and infinities clamped (sanitize).  Thread t holds the
-// scores of blocks [base, base + IPT) in v and their content bits in
-// `content`; L.maxv[0, n_max) (n_max <= NT) holds the content maxima of
-// disjoint sub-chunks (or -inf), written before a barrier, and L is
-// select_init'ed.  Calls emit(r, block) for every rank r < KC (KC >= 1).
-// Called by all NT threads.
+// Selection of the KC largest content scores of a head, by (score desc,
+// block asc), with NaN ranked last and infinities clamped (sanitize), in two
+// steps.
 //
-// A threshold tau comes first: two radix passes over the order-preserving
-// keys of the maxima (top byte, then the next byte within the bin that holds
-// the KC-th largest) give the 16-bit key prefix of the KC-th largest maximum;
-// tau is the smallest float with that prefix.  Those KC maxima are KC distinct
-// content scores >= tau, so every one of the top KC is >= tau; maxima left
-// out only lower tau.  The candidates (content scores >= tau) are compacted
-// and, when at most kSortCap survive, ranked exactly by all-pairs comparison;
-// otherwise linear-bin radix passes refine the boundary and a bitonic sort
-// orders the survivors.
+// select_threshold, by one wave (no workgroup barrier inside): a threshold
+// tau from L.maxv[0, n_max) (n_max <= NT), the content maxima of disjoint
+// sub-chunks (or -inf), written before a barrier.  Two radix passes over the
+// order-preserving keys of the maxima (top byte, then the next byte within
+// the bin that holds the KC-th largest) give the 16-bit key prefix of the
+// KC-th largest maximum; tau is the smallest float with that prefix.  Those
+// KC maxima are KC distinct content scores >= tau, so every one of the top KC
+// is >= tau; maxima left out only lower tau.  L is select_init'ed.
+template <int NT>
+__device__ void select_threshold(SelectLds<NT>& L, int KC, int n_max) {
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int i = lane; i < n_max; i += kWave) {
+    const float mv = L.maxv[i];
+    if (mv != -INFINITY) atomicAdd(&L.rh[(uint32_t)(sel_key(mv, 0) >> 32) >> 24], 1);
+  }
+  __builtin_amdgcn_wave_barrier();             // a wave's LDS operations complete in order
+  radix_digit(L.rh, KC, L.bc);                 // bc[0] = digit, bc[1] = count above
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t b1 = (uint32_t)L.bc[0];
+  const int above1 = L.bc[1];
+  for (int i = lane; i < n_max; i += kWave) {
+    const float mv = L.maxv[i];
+    const uint32_t key = (uint32_t)(sel_key(mv, 0) >> 32);
+    if (mv != -INFINITY && (key >> 24) == b1) atomicAdd(&L.rh[256 + ((key >> 16) & 0xffu)], 1);
+  }
+  __builtin_amdgcn_wave_barrier();
+  radix_digit(L.rh + 256, KC - above1, L.bc + 2);
+  __builtin_amdgcn_wave_barrier();
+  if (lane == 0) {
+    const uint32_t tk = (b1 << 24) | ((uint32_t)L.bc[2] << 16);
+    const uint32_t u = (tk & 0x80000000u) ? (tk & 0x7fffffffu) : ~tk;
+    L.tau = (above1 < 0 || L.bc[3] < 0) ? -FLT_MAX : fmaxf(__uint_as_float(u), -FLT_MAX);
+  }
+}
+
+// select_content, by all NT threads after a barrier that follows
+// select_threshold: thread t holds the scores of blocks [base, base + IPT)
+// in v and their content bits in `content`.  The candidates (content scores
+// >= tau) are compacted -- only threads holding one take part -- and, when at
+// most kSortCap survive, ranked exactly by all-pairs comparison; otherwise
+// linear-bin radix passes refine the boundary and a bitonic sort orders the
+// survivors.  Calls emit(r, block) for every rank r < KC (KC >= 1).
 template <int NT, int IPT, typename Emit>
 __device__ void select_content(SelectLds<NT>& L, float (&v)[IPT], MaskT<IPT> content, int base, int KC,
-                               int n_max, Emit&& emit) {
+                               Emit&& emit) {
   using Mask = MaskT<IPT>;
   constexpr Mask kOne = 1;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
-  {
-    const bool has_max = tid < n_max && L.maxv[tid] != -INFINITY;
-    const uint32_t key = has_max ? (uint32_t)(sel_key(L.maxv[tid], 0) >> 32) : 0u;
-    if (has_max) atomicAdd(&L.rh[key >> 24], 1);
-    __syncthreads();
-    if (w == 0) radix_digit(L.rh, KC, L.bc);          // bc[0] = digit, bc[1] = count above
-    __syncthreads();
-    const uint32_t b1 = (uint32_t)L.bc[0];
-    const int above1 = L.bc[1];
-    if (has_max && (key >> 24) == b1) atomicAdd(&L.rh[256 + ((key >> 16) & 0xffu)], 1);
-    __syncthreads();
-    if (w == 0) {
-      radix_digit(L.rh + 256, KC - above1, L.bc + 2);
-      if (lane == 0) {
-        const uint32_t tk = (b1 << 24) | ((uint32_t)L.bc[2] << 16);
-        const uint32_t u = (tk & 0x80000000u) ? (tk & 0x7fffffffu) : ~tk;
-        L.tau = (above1 < 0 || L.bc[3] < 0) ? -FLT_MAX : fmaxf(__uint_as_float(u), -FLT_MAX);
-      }
-    }
-  }
-  __syncthreads();
-
-  // ---- candidates: content scores >= tau, one LDS atomic per wave ----
+  const int tid = threadIdx.x;
   const float tau = L.tau;
   Mask cm = 0;
   if (tau == -FLT_MAX) {                       // the bottom of the range: compare sanitised scores
@@ -234,21 +240,13 @@ __device__ void select_content(SelectLds<NT>& L, float (&v)[IPT], MaskT<IPT> con
     for (int i = 0; i < IPT; ++i) cm |= (v[i] >= tau) ? (kOne << i) : Mask(0);
   }
   cm &= content;
-  {
-    const int c = popcnt(cm);
-    const int inc = wave_incl_scan(c);
-    const int wtot = __builtin_amdgcn_readlane(inc, kWave - 1);
-    if (wtot) {
-      int o0 = 0;
-      if (lane == kWave - 1) o0 = atomicAdd(&L.n, wtot);
-      int o = __builtin_amdgcn_readlane(o0, kWave - 1) + inc - c;
+  if (cm) {                                    // few threads hold a candidate
+    int o = atomicAdd(&L.n, popcnt(cm));
 #pragma unroll
-      for (int i = 0; i < IPT; ++i) {
-        const bool bit = (cm >> i) & kOne;
-        if (__ballot(bit)) {                   // most element positions hold no candidate in the wave
-          if (bit && o < kSortCap) L.keys[o] = sel_key(sanitize(v[i]), base + i);
-          o += bit ? 1 : 0;
-        }
+    for (int i = 0; i < IPT; ++i) {
+      if ((cm >> i) & kOne) {
+        if (o < kSortCap) L.keys[o] = sel_key(sanitize(v[i]), base + i);
+        ++o;
       }
     }
   }
