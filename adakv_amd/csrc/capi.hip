@@ -165,6 +165,8 @@ ScoreArgs score_args(const adakv_geometry_t* g, const adakv_query_t* q, const ad
   sa.seq_lens = lens; sa.uniform_len = g->max_seq_len; sa.bs = g->block_size;
   sa.B = g->batch; sa.Hq = g->n_q_heads; sa.Hkv = g->n_kv_heads; sa.G = g->n_q_heads / g->n_kv_heads;
   sa.scores = scores; sa.sp = sp;
+  sa.q_vec = q->dtype == c->dtype && q->dtype != ADAKV_F32 && aligned16(q->data) && q->stride_b % 8 == 0 &&
+             q->stride_h % 8 == 0;
   return sa;
 }
 

@@ -43,6 +43,7 @@ struct ScoreArgs {
   int parts_pitch;
   BudgetCfg cfg;
   int n_app, n_chunks, chunk_rows;   // set by the launcher
+  int q_vec;                   // 1: q has the centroid type and 16-byte aligned rows (vector loads)
 };
 
 // Softmax record of a score workgroup's rows for one head (z = score /

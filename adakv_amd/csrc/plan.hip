@@ -31,6 +31,7 @@ namespace adakv {
 namespace {
 
 constexpr int kNT = 256;
+constexpr int kScoreTiles = 4;   // 16-row centroid tiles per wave of the matrix-core scan
 
 __device__ __forceinline__ float round_to(float x, int dt) {
   if (dt == ADAKV_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(x));
@@ -223,7 +224,7 @@ __device__ void score_chunk_mfma(const ScoreArgs& a, int b, int kvh, int unit, i
                                  float (*s_pm)[GMAX][4]) {
   static_assert(D % 32 == 0 && GMAX <= 16, "16x16 tiles over head_dim");
   constexpr int KS = D / 32;                // k-steps (16-byte loads per lane per tile)
-  constexpr int TPW = 4;                    // tiles per wave
+  constexpr int TPW = kScoreTiles;          // tiles per wave
   constexpr int RPW = 16 * TPW;             // rows per wave = rows per sub-chunk
   constexpr int NWV = kNT / kWave;
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
@@ -234,6 +235,17 @@ __device__ void score_chunk_mfma(const ScoreArgs& a, int b, int kvh, int unit, i
   const bool wave_on = wrow0 < nrows;       // uniform over the wave
   float m = -INFINITY, S = 0.f, T = 0.f, hi = -INFINITY;
   if (wave_on) {
+    // B fragments: lane (col, grp) holds q[head col][32s + 8grp .. +7] (columns
+    // col >= G repeat the last head; their scores are never stored).  With q of
+    // the centroid type and 16-byte aligned rows they are plain 16-byte loads,
+    // issued first; otherwise typed loads after the centroid loads.
+    uint4 qf[KS];
+    const int64_t qo = (int64_t)b * a.qsb + (int64_t)(kvh * G + min(col, G - 1)) * a.qsh + 8 * grp;
+    if (a.q_vec) {
+      const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) + qo;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) qf[s] = *reinterpret_cast<const uint4*>(qp + 32 * s);
+    }
     // A fragments: lane (col, grp) reads row wrow0 + 16t + col, elements
     // [32s + 8grp, 32s + 8grp + 8) at k-step s, so that the 4 lanes of a row
     // read one whole 64-byte segment per load instruction
@@ -246,24 +258,23 @@ __device__ void score_chunk_mfma(const ScoreArgs& a, int b, int kvh, int unit, i
 #pragma unroll
       for (int s = 0; s < KS; ++s) cf[t][s] = load16(cbase + (int64_t)r * D * 2 + 64 * s);
     }
-    // B fragments: lane (col, grp) holds q[head col][32s + 8grp .. +7]
-    uint4 qf[KS];
-    with_dtype(a.qdt, [&](auto tag) {
-      constexpr int QDT = decltype(tag)::value;
-      const int64_t qo = (int64_t)b * a.qsb + (int64_t)(kvh * G + min(col, G - 1)) * a.qsh + 8 * grp;
-      float x[KS][8];
+    if (!a.q_vec) {
+      with_dtype(a.qdt, [&](auto tag) {
+        constexpr int QDT = decltype(tag)::value;
+        float x[KS][8];
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
+        for (int s = 0; s < KS; ++s)
 #pragma unroll
-        for (int u = 0; u < 8; ++u) x[s][u] = load_t<QDT>(a.q, qo + 32 * s + u);
+          for (int u = 0; u < 8; ++u) x[s][u] = load_t<QDT>(a.q, qo + 32 * s + u);
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        uint32_t wv[4];
+        for (int s = 0; s < KS; ++s) {
+          uint32_t wv[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) wv[u] = col < G ? pack2_typed<CDT>(x[s][2 * u], x[s][2 * u + 1]) : 0u;
-        qf[s] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
-      }
-    });
+          for (int u = 0; u < 4; ++u) wv[u] = pack2_typed<CDT>(x[s][2 * u], x[s][2 * u + 1]);
+          qf[s] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+        }
+      });
+    }
     float sc[TPW][4];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
@@ -520,8 +531,8 @@ hipError_t launch_score_d(ScoreArgs& a, hipStream_t s) {
     a.chunk_rows = CB;
     a.n_chunks = (a.max_blocks + CB - 1) / CB;
   } else {
-    a.chunk_rows = 4 * 64;                                      // 4 waves of 64 rows per record
-    a.n_chunks = (a.max_blocks + 4 * 64 - 1) / (4 * 64);
+    a.chunk_rows = 4 * 16 * kScoreTiles;                        // 4 waves of 16-row tiles per record
+    a.n_chunks = (a.max_blocks + a.chunk_rows - 1) / a.chunk_rows;
   }
   // blocks holding the newest n_new tokens: at most ceil(n_new / bs) + 1
   a.n_app = a.n_new > 0 ? std::min((a.n_new + a.bs - 1) / a.bs + 1, a.max_blocks) : 0;
