@@ -258,17 +258,31 @@ __device__ void select_content(SelectLds<NT>& L, float (&v)[IPT], MaskT<IPT> con
     __syncthreads();
     const int n2 = (n_cand + 1) & ~1;
     const int npad = next_pow2(max(n_cand, 1));
-    const int parts = max(NT / npad, 1), jlen = (ceil_div(n2, parts) + 1) & ~1;
-    const int i = tid % npad, j0 = (tid / npad) * jlen, j1 = min(n2, j0 + jlen);
-    if (i < n_cand && tid / npad < parts) {
-      const uint64_t ki = L.keys[i];
-      int r = 0;
+    if (npad <= NT) {
+      // NT / npad threads per candidate, each over a slice of the others
+      const int parts = NT / npad, jlen = (ceil_div(n2, parts) + 1) & ~1;
+      const int i = tid % npad, j0 = (tid / npad) * jlen, j1 = min(n2, j0 + jlen);
+      if (i < n_cand) {
+        const uint64_t ki = L.keys[i];
+        int r = 0;
 #pragma unroll 4
-      for (int j = j0; j < j1; j += 2) {
-        const ulonglong2 y = *reinterpret_cast<const ulonglong2*>(&L.keys[j]);
-        r += (y.x > ki) + (y.y > ki);
+        for (int j = j0; j < j1; j += 2) {
+          const ulonglong2 y = *reinterpret_cast<const ulonglong2*>(&L.keys[j]);
+          r += (y.x > ki) + (y.y > ki);
+        }
+        if (r) atomicAdd(&L.rank[i], r);
       }
-      if (r) atomicAdd(&L.rank[i], r);
+    } else {
+      // more candidates than threads: each thread ranks several against all
+      for (int i = tid; i < n_cand; i += NT) {
+        const uint64_t ki = L.keys[i];
+        int r = 0;
+        for (int j = 0; j < n2; j += 2) {
+          const ulonglong2 y = *reinterpret_cast<const ulonglong2*>(&L.keys[j]);
+          r += (y.x > ki) + (y.y > ki);
+        }
+        L.rank[i] = r;
+      }
     }
     __syncthreads();
     for (int e = tid; e < n_cand; e += NT)
