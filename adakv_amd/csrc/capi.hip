@@ -440,12 +440,13 @@ int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const 
   int32_t* lens = sel ? sel->sel_lens : reinterpret_cast<int32_t*>(w + L.lens);
   const hipStream_t s = (hipStream_t)stream;
   if (append_new > 0 && !centroid_pair_ok(kv->dtype, c->dtype)) return ADAKV_ERR_DTYPE;
-  // bf16 / fp16 K/V (and q of the same type) on a shape the fused kernel
+  // bf16 / fp16 K/V (and q of the same type, 16-byte aligned rows) on a shape the fused kernel
   // serves: scores, then one kernel for the budget, the selection and the
   // decode of every head
-  if (kv->dtype != ADAKV_F32 && q->dtype == kv->dtype &&
+  if (kv->dtype != ADAKV_F32 && q->dtype == kv->dtype && aligned16(q->data) && q->stride_b % 8 == 0 &&
+      q->stride_h % 8 == 0 &&
       select_decode_supported(g->head_dim, g->max_blocks, T, g->n_q_heads, L.sp, L.parts_pitch) &&
-      select_decode_lds(g->head_dim, g->n_q_heads) <= max_lds_per_block()) {
+      select_decode_lds(g->head_dim, g->n_q_heads, g->max_blocks) <= max_lds_per_block()) {
     FusedArgs fa{};
     if ((st = run_scores(g, q, c, kv, append_new, seq_lens, p, table, Tl, w, s, &fa.s))) return st;
     fa.d = decode_args(g, q, kv, seq_lens, sm_scale, out);

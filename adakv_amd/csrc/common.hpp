@@ -213,6 +213,15 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
   return x + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
 }
 
+// Workgroup barrier for data exchanged through LDS only: it waits for this
+// wave's LDS operations but not for its outstanding global loads (the
+// workgroup fence of __syncthreads waits for those too), so loads issued
+// before it stay in flight.  The memory clobber keeps the compiler from moving
+// memory accesses across it.  Not for global-memory hand-offs between waves.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // ---- workgroup reductions (NT threads, scratch of >= NT/64 slots) ------------
 template <int NT, typename T, typename Op>
 __device__ __forceinline__ T block_reduce(T x, T* scratch, Op op) {

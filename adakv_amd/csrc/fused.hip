@@ -41,16 +41,24 @@ constexpr int kRecsPerLane = 4;              // records a lane loads up front
 template <int D>
 constexpr int fused_decode_waves() { return kFusedThreads / kWave; }
 
-template <int D>
+template <int D, int IPT>
 union FusedBig {
-  SelectLds<kFusedThreads> sel;                                    // the selection
+  struct {
+    SelectLds<kFusedThreads> sel;                                  // the selection
+    alignas(16) float sc[kFusedThreads * IPT];                     // and this head's scores
+  } x;
   uint32_t vt[fused_decode_waves<D>() * TileShape<D>::VT_WORDS];   // then the V tiles
-  float acc[fused_decode_waves<D>()][D];                           // then the merge
 };
 
-template <int D>
+template <int D, int IPT>
 constexpr size_t fused_static_lds() {
-  return sizeof(FusedBig<D>) + kSortCap * sizeof(int) + 2 * fused_decode_waves<D>() * sizeof(float);
+  return sizeof(FusedBig<D, IPT>) + kSortCap * sizeof(int) + (2 + D) * fused_decode_waves<D>() * sizeof(float);
+}
+
+// Scores per thread for a max_blocks (0: not served).
+inline int fused_ipt(int max_blocks) {
+  return max_blocks <= kFusedThreads * 4 ? 4 : max_blocks <= kFusedThreads * 8 ? 8
+       : max_blocks <= kFusedThreads * 16 ? 16 : 0;
 }
 
 // x / d, with s = log2(d) when d is a power of two (else -1).
@@ -96,9 +104,10 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
   constexpr int LPH = kLanesPerHead, HPW = kWave / LPH, RPL = kRecsPerLane;
   using Mask = MaskT<IPT>;
   constexpr Mask kOne = 1;
-  __shared__ __align__(16) FusedBig<D> big;
+  __shared__ __align__(16) FusedBig<D, IPT> big;
   __shared__ int s_list[kSortCap];          // content blocks by rank
   __shared__ float s_m[DW], s_l[DW];
+  __shared__ float s_acc[DW][D];            // the decode waves' accumulators for the merge
   extern __shared__ double s_w[];            // [Hq] entropy weights of the sequence's heads
 
   const SelectArgs& a = fa.s;
@@ -122,7 +131,7 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
     for (int i = tid; i < D; i += NT) store_elt(d.out, d.odt, oo + i, __builtin_nanf(""));
     return;
   }
-  select_init(big.sel);
+  select_init(big.x.sel);
 
   // ---- 1. loads ----
   // Every load here is unconditional, its index clamped in bounds (values not
@@ -172,20 +181,19 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
     }
   }
   __builtin_amdgcn_sched_barrier(0);
-  // (c) the query (same 16-bit type as K), raw until the decode: lane (col,
-  //     grp) holds q[D/4*grp + 8*s + t]
-  uint32_t qraw[D / 32][8];
+  // (c) the query (same 16-bit type as K, 16-byte aligned rows), as the B
+  //     operand of S^T: lane (col, grp) holds q[D/4*grp + 8*s .. +7] in
+  //     every column (columns other than 0 are masked out of the softmax)
+  uint4 qf[D / 32];
   {
     const uint16_t* qp = reinterpret_cast<const uint16_t*>(d.q) + (int64_t)b * d.qsb + (int64_t)h * d.qsh + (D / 4) * grp;
 #pragma unroll
-    for (int s2 = 0; s2 < D / 32; ++s2)
-#pragma unroll
-      for (int t = 0; t < 8; ++t) qraw[s2][t] = qp[8 * s2 + t];
+    for (int s2 = 0; s2 < D / 32; ++s2) qf[s2] = *reinterpret_cast<const uint4*>(qp + 8 * s2);
   }
   __builtin_amdgcn_sched_barrier(0);
-  // (d) the forced tiles: item i (16-token sub-tile i % n_sub of list entry
-  //     i / n_sub) belongs to decode wave i % DW; the first n_forced entries
-  //     are the sink blocks then the local blocks, as in the table row
+  // (d) the decode's addressing: item i (16-token sub-tile i % n_sub of list
+  //     entry i / n_sub) belongs to decode wave i % DW; the first n_forced
+  //     entries are the sink blocks then the local blocks, as in the table row
   const int n_sub = (a.bs + 15) >> 4;
   const int nf_items = nf * n_sub;
   const int64_t head_off = ((int64_t)b * d.sb + (int64_t)(h / d.G) * d.sh + (D / 4) * grp) * 2;
@@ -198,11 +206,14 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
     t0 = blk * a.bs + sub * 16;
     t_hi = min(min(blk * a.bs + a.bs, len), t0 + 16);
   };
-  const bool pre = w < DW && w < nf_items;   // uniform over the wave
+  // the forced tiles of the prefetch path (below): known before any selection
+  const int wu = __builtin_amdgcn_readfirstlane(w);   // the wave index, provably uniform
+  const bool pf_shape = n_sub == 1 && nf <= DW;
+  const bool p_load = pf_shape && wu < nf;
   TileBuf<D> P;
   int p0 = 0, p1 = 1;
-  if (pre) {
-    item(w, p0, p1);
+  if (p_load) {
+    item(wu, p0, p1);
     tile_load<D>(kbase, vbase, row_bytes, p0, p1, P);
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -210,22 +221,9 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
 
   // ---- 2. entropy weights and this head's content maxima ----
   // Maxima of record j at 4j .. 4j+3, of row e no record covers at 4*n_ck + e.
-  const int passes = adaptive ? ceil_div(Hq, HPW * NW) : 1;
-  for (int p = 0; p < passes; ++p) {
-    const int hh = head_of(p);
+  // one head per 16-lane row: merge its records (and rows no record covers)
+  auto merge_head = [&](int hh, const float4 (&Q0)[RPL], const float4 (&Q1)[RPL], float X) {
     const bool on = hh >= 0 && hh < Hq;
-    const int hs = on ? hh : h;
-    float4 Q0[RPL], Q1[RPL];
-    float X;
-    if (p == 0) {
-#pragma unroll
-      for (int u = 0; u < RPL; ++u) { Q0[u] = R0[u]; Q1[u] = R1[u]; }
-      X = X0;
-    } else {
-#pragma unroll
-      for (int u = 0; u < RPL; ++u) { Q0[u] = rec(hs, hl + LPH * u)[0]; Q1[u] = rec(hs, hl + LPH * u)[1]; }
-      X = *extra(hs, hl);
-    }
     SoftPart pt = soft_empty();
     if (on) {
       const bool own = hh == h;
@@ -235,13 +233,13 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
           const float mx[4] = {q0.w, q1.x, q1.y, q1.z};
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (4 * j + i < NT) big.sel.maxv[4 * j + i] = mx[i];
+            if (4 * j + i < NT) big.x.sel.maxv[4 * j + i] = mx[i];
         }
       };
       auto take_row = [&](int e, float x) {
         pt = soft_merge(pt, SoftPart{tf == 1.f ? x : __fdiv_rn(x, tf), 1.f, 0.f});
         const int r = rows_in_chunks + e, t = 4 * n_ck + e;
-        if (own && t < NT) big.sel.maxv[t] = (r >= c_lo && r < c_hi) ? sanitize(x) : -INFINITY;
+        if (own && t < NT) big.x.sel.maxv[t] = (r >= c_lo && r < c_hi) ? sanitize(x) : -INFINITY;
       };
 #pragma unroll
       for (int u = 0; u < RPL; ++u)
@@ -252,8 +250,34 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
     }
     pt = soft_group_merge<LPH>(pt);
     if (adaptive && on && hl == 0) s_w[hh] = entropy_weight(pt, lognb);
+  };
+  // the first pass consumes the records loaded up front, in place
+  merge_head(hh0, R0, R1, X0);
+  const int passes = adaptive ? ceil_div(Hq, HPW * NW) : 1;
+  for (int p = 1; p < passes; ++p) {         // more than 32 heads
+    const int hh = head_of(p);
+    const int hs = (hh >= 0 && hh < Hq) ? hh : h;
+    float4 Q0[RPL], Q1[RPL];
+#pragma unroll
+    for (int u = 0; u < RPL; ++u) { Q0[u] = rec(hs, hl + LPH * u)[0]; Q1[u] = rec(hs, hl + LPH * u)[1]; }
+    merge_head(hh, Q0, Q1, *extra(hs, hl));
   }
-  __syncthreads();
+  // this head's scores to LDS (the selection reads them there, so they hold
+  // no registers while the tiles are prefetched), this thread's content bits
+  // and its largest sanitised content score
+  const int base = tid * IPT;
+  Mask content = 0;
+  float vmax = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const bool is_c = base + i >= c_lo && base + i < c_hi;
+    if (is_c) content |= kOne << i;
+    vmax = fmaxf(vmax, is_c ? sanitize(v[i]) : -INFINITY);
+  }
+#pragma unroll
+  for (int i = 0; i < IPT; i += 4)
+    *reinterpret_cast<float4*>(&big.x.sc[base + i]) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+  lds_barrier();
 
   // ---- 3. the head's count and selection ----
   // every wave evaluates the sum of weights in NumPy's order
@@ -266,35 +290,44 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
   const int KC = max(k - nf, 0);
   for (int j = tid; j < nf; j += NT) trow[j] = j < bb.sink ? j : local_lo + (j - bb.sink);
   for (int j = k + tid; j < a.T; j += NT) trow[j] = -1;
+  // Prefetch: with one tile per block, the forced blocks on their own waves
+  // and at most DW candidates, wave w holds forced block w (w < nf, loaded in
+  // the prologue) and loads candidate (w - nf) mod DW as soon as the
+  // candidates are known, before they are ranked; after the rank it computes
+  // the candidate if its rank is < KC (the decode does not depend on the
+  // order of the blocks).  Only the waves that own a tile issue loads.
+  bool prefetched = false;
+  TileBuf<D> C;
+  int c0 = 0, c1 = 1, cand = -1;
   if (KC > 0) {
-    if (w == 0) select_threshold(big.sel, KC, min(4 * n_ck + n_extra, NT));
-    __syncthreads();
-    const int base = tid * IPT;
-    Mask content = 0;
-#pragma unroll
-    for (int i = 0; i < IPT; ++i)
-      if (base + i >= c_lo && base + i < c_hi) content |= kOne << i;
-    select_content<NT, IPT>(big.sel, v, content, base, KC, [&](int r, int blk) {
-      s_list[r] = blk;
-      trow[nf + r] = blk;
-    });
+    if (w == 0) select_threshold(big.x.sel, KC, min(4 * n_ck + n_extra, NT));
+    lds_barrier();
+    select_content<NT, IPT>(
+        big.x.sel, [&](int i) { return big.x.sc[base + i]; }, content, base, KC, vmax,
+        [&](int r, int blk) {
+          s_list[r] = blk;
+          trow[nf + r] = blk;
+        },
+        [&](int n_cand) {
+          prefetched = pf_shape && n_cand <= DW;
+          const int c = (wu - nf % DW + DW) % DW;
+          if (prefetched && wu < DW && c < n_cand) {
+            const int blk = key_index(big.x.sel.keys[c]);
+            c0 = blk * a.bs;
+            c1 = min(c0 + a.bs, len);
+            tile_load<D>(kbase, vbase, row_bytes, c0, c1, C);
+            cand = c;
+          }
+        });
   }
-  __syncthreads();                           // s_list complete; the selection's LDS becomes the V tiles
+  const bool c_take = cand >= 0 && big.x.sel.rank[cand] < KC;   // read before the LDS is reused
+  lds_barrier();                           // s_list complete; the selection's LDS becomes the V tiles
 
   // ---- 4. flash-decode over the k blocks ----
   TileState<D> st;
   tile_init(st);
   const int n_items = k * n_sub;
   if (w < DW) {
-    // B operand of S^T: the head in column 0, the other columns zero
-    uint4 qf[D / 32];
-#pragma unroll
-    for (int s2 = 0; s2 < D / 32; ++s2) {
-      uint32_t wv[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) wv[t] = col == 0 ? (qraw[s2][2 * t] | (qraw[s2][2 * t + 1] << 16)) : 0u;
-      qf[s2] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
-    }
     uint32_t* vt = big.vt + w * TileShape<D>::VT_WORDS;
     const float scale = d.scale_log2;
     auto load = [&](int t0, int t_hi, TileBuf<D>& r) { tile_load<D>(kbase, vbase, row_bytes, t0, t_hi, r); };
@@ -302,18 +335,18 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
       tile_update<KVDT, D>(st, r, qf, vt, t0, t_hi, col == 0, scale);
     };
     const int mine = w < n_items ? (n_items - w + DW - 1) / DW : 0;   // items of this wave
-    if (mine > 0) {
-      // item w is the prefetched forced tile when `pre`; later items are
-      // loaded now, at most two in flight, each load issued for an item
-      // the wave computes
+    if (prefetched) {
+      // forced tile (item w) and the wave's candidate, both loaded earlier
+      __builtin_amdgcn_sched_barrier(0);
+      if (p_load) compute(p0, p1, P);
+      if (c_take) compute(c0, c1, C);
+    } else if (mine > 0) {
+      // items loaded now, at most two in flight, each load issued for an
+      // item the wave computes
       TileBuf<D> A, B;
       int a0, a1, b0, b1;
-      if (pre) {
-        A = P; a0 = p0; a1 = p1;
-      } else {
-        item(w, a0, a1);
-        load(a0, a1, A);
-      }
+      item(w, a0, a1);
+      load(a0, a1, A);
       if (mine == 1) {
         __builtin_amdgcn_sched_barrier(0);
         compute(a0, a1, A);
@@ -356,12 +389,11 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
     s_m[w] = st.m_h;
     s_l[w] = st.l_h;
   }
-  __syncthreads();                           // the V tiles are dead: merge through the same LDS
   if (w < DW && grp == 0) {
 #pragma unroll
-    for (int n = 0; n < NT16; ++n) big.acc[w][n * 16 + col] = st.acc[n][0];   // O[head 0][16n + col]
+    for (int n = 0; n < NT16; ++n) s_acc[w][n * 16 + col] = st.acc[n][0];   // O[head 0][16n + col]
   }
-  __syncthreads();
+  lds_barrier();
   for (int i = tid; i < D; i += NT) {
     float M = -INFINITY;
 #pragma unroll
@@ -372,7 +404,7 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
       for (int ww = 0; ww < DW; ++ww) {
         const float f = s_m[ww] == -INFINITY ? 0.f : exp2f(s_m[ww] - M);
         L += s_l[ww] * f;
-        O += big.acc[ww][i] * f;
+        O += s_acc[ww][i] * f;
       }
     }
     store_elt(d.out, d.odt, oo + i, O / L);   // no block at all: 0/0 as the reference kernel
@@ -383,14 +415,12 @@ template <int KVDT, int D>
 hipError_t launch_fd(const FusedArgs& a, int max_blocks, hipStream_t s) {
   const dim3 grid(a.s.Hq, a.s.B);
   const size_t dyn = (size_t)a.s.Hq * sizeof(double);
-  if (max_blocks <= kFusedThreads * 4)
-    hipLaunchKernelGGL((select_decode_kernel<KVDT, D, 4>), grid, dim3(kFusedThreads), dyn, s, a);
-  else if (max_blocks <= kFusedThreads * 8)
-    hipLaunchKernelGGL((select_decode_kernel<KVDT, D, 8>), grid, dim3(kFusedThreads), dyn, s, a);
-  else if (max_blocks <= kFusedThreads * 16)
-    hipLaunchKernelGGL((select_decode_kernel<KVDT, D, 16>), grid, dim3(kFusedThreads), dyn, s, a);
-  else
-    return hipErrorInvalidValue;
+  switch (fused_ipt(max_blocks)) {
+    case 4: hipLaunchKernelGGL((select_decode_kernel<KVDT, D, 4>), grid, dim3(kFusedThreads), dyn, s, a); break;
+    case 8: hipLaunchKernelGGL((select_decode_kernel<KVDT, D, 8>), grid, dim3(kFusedThreads), dyn, s, a); break;
+    case 16: hipLaunchKernelGGL((select_decode_kernel<KVDT, D, 16>), grid, dim3(kFusedThreads), dyn, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
@@ -414,15 +444,26 @@ bool select_decode_supported(int D, int max_blocks, int table_width, int Hq, int
          (int64_t)Hq * sp < (1ll << 31) && (int64_t)Hq * parts_pitch * kPartFloats < (1ll << 31);
 }
 
-size_t select_decode_lds(int D, int Hq) {
-  size_t st = 0;
-  switch (D) {
-    case 32: st = fused_static_lds<32>(); break;
-    case 64: st = fused_static_lds<64>(); break;
-    case 128: st = fused_static_lds<128>(); break;
+template <int D>
+size_t fused_lds_d(int ipt) {
+  switch (ipt) {
+    case 4: return fused_static_lds<D, 4>();
+    case 8: return fused_static_lds<D, 8>();
+    case 16: return fused_static_lds<D, 16>();
     default: return (size_t)-1;
   }
-  return st + (size_t)Hq * sizeof(double);
+}
+
+size_t select_decode_lds(int D, int Hq, int max_blocks) {
+  const int ipt = fused_ipt(max_blocks);
+  size_t st = 0;
+  switch (D) {
+    case 32: st = fused_lds_d<32>(ipt); break;
+    case 64: st = fused_lds_d<64>(ipt); break;
+    case 128: st = fused_lds_d<128>(ipt); break;
+    default: return (size_t)-1;
+  }
+  return st == (size_t)-1 ? st : st + (size_t)Hq * sizeof(double);
 }
 
 hipError_t launch_select_decode(const FusedArgs& a, int kvdt, int D, int max_blocks, hipStream_t s) {

@@ -494,7 +494,8 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
     const int nf = bb.n_forced;
     if (w == 0) select_threshold(L, KC, n_max);
     __syncthreads();
-    select_content<NT, IPT>(L, v, content, base, KC, [&](int r, int blk) { trow[nf + r] = blk; });
+    select_content<NT, IPT>(L, [&](int i) { return v[i]; }, content, base, KC, INFINITY,
+                            [&](int r, int blk) { trow[nf + r] = blk; }, [](int) {});
   }
   // the head's entropy weight from the waves' partials (adakv/budget.py:33-37)
   if (adaptive && w == NW - 1) {

@@ -14,6 +14,7 @@
 namespace adakv {
 
 constexpr int kSortCap = 512;       // candidates ranked exactly by all-pairs comparison
+constexpr int kSmallKC = 16;        // up to this many, the threshold is found by repeated wave maxima
 
 // NaN ranks last, infinities clamp to the finite range (they then tie with
 // +/-FLT_MAX and are ordered by block index).
@@ -187,12 +188,44 @@ __device__ __forceinline__ void radix_digit(const int* hist, int need, int* out)
 // sub-chunks (or -inf), written before a barrier.  Two radix passes over the
 // order-preserving keys of the maxima (top byte, then the next byte within
 // the bin that holds the KC-th largest) give the 16-bit key prefix of the
-// KC-th largest maximum; tau is the smallest float with that prefix.  Those
-// KC maxima are KC distinct content scores >= tau, so every one of the top KC
-// is >= tau; maxima left out only lower tau.  L is select_init'ed.
+// KC-th largest maximum; tau is the smallest float with that prefix (for
+// KC <= kSmallKC, tau is that maximum itself).  Those KC maxima are KC
+// distinct content scores >= tau, so every one of the top KC is >= tau;
+// maxima left out only lower tau.  L is select_init'ed.
 template <int NT>
 __device__ void select_threshold(SelectLds<NT>& L, int KC, int n_max) {
   const int lane = threadIdx.x & (kWave - 1);
+  if (KC <= kSmallKC) {
+    // small KC: the exact KC-th largest maximum, by KC rounds of a wave max
+    // that removes one occurrence each (so equal maxima count separately)
+    constexpr int PER = NT / kWave;
+    float mv[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) mv[i] = lane + kWave * i < n_max ? L.maxv[lane + kWave * i] : -INFINITY;
+    float kth = -INFINITY;
+    int found = 0;
+    for (int r = 0; r < KC; ++r) {
+      float lm = mv[0];
+#pragma unroll
+      for (int i = 1; i < PER; ++i) lm = fmaxf(lm, mv[i]);
+      const float wm = wave_allreduce(lm, OpMax());
+      if (wm == -INFINITY) break;                         // fewer than KC maxima
+      const uint64_t holders = __ballot(lm == wm);
+      if (lane == (int)__builtin_ctzll(holders)) {
+        bool done = false;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const bool hit = !done && mv[i] == wm;
+          mv[i] = hit ? -INFINITY : mv[i];
+          done = done || hit;
+        }
+      }
+      kth = wm;
+      ++found;
+    }
+    if (lane == 0) L.tau = found == KC ? fmaxf(kth, -FLT_MAX) : -FLT_MAX;
+    return;
+  }
   for (int i = lane; i < n_max; i += kWave) {
     const float mv = L.maxv[i];
     if (mv != -INFINITY) atomicAdd(&L.rh[(uint32_t)(sel_key(mv, 0) >> 32) >> 24], 1);
@@ -218,44 +251,50 @@ __device__ void select_threshold(SelectLds<NT>& L, int KC, int n_max) {
 }
 
 // select_content, by all NT threads after a barrier that follows
-// select_threshold: thread t holds the scores of blocks [base, base + IPT)
-// in v and their content bits in `content`.  The candidates (content scores
+// select_threshold: get(i) is the score of block base + i (i < IPT, a
+// constant in unrolled loops) of thread t, `content` its content bits; vmax >= the largest sanitised
+// content score among them (a thread with vmax < tau holds no candidate and
+// skips the comparisons).  on_cand(n_cand) runs right after the candidates
+// are compacted in L.keys (before they are ranked), by every thread.  The candidates (content scores
 // >= tau) are compacted -- only threads holding one take part -- and, when at
 // most kSortCap survive, ranked exactly by all-pairs comparison; otherwise
 // linear-bin radix passes refine the boundary and a bitonic sort orders the
 // survivors.  Calls emit(r, block) for every rank r < KC (KC >= 1).
-template <int NT, int IPT, typename Emit>
-__device__ void select_content(SelectLds<NT>& L, float (&v)[IPT], MaskT<IPT> content, int base, int KC,
-                               Emit&& emit) {
+template <int NT, int IPT, typename Get, typename Emit, typename OnCand>
+__device__ void select_content(SelectLds<NT>& L, Get&& get, MaskT<IPT> content, int base, int KC,
+                               float vmax, Emit&& emit, OnCand&& on_cand) {
   using Mask = MaskT<IPT>;
   constexpr Mask kOne = 1;
   const int tid = threadIdx.x;
   const float tau = L.tau;
   Mask cm = 0;
-  if (tau == -FLT_MAX) {                       // the bottom of the range: compare sanitised scores
+  if (vmax >= tau) {
+    if (tau == -FLT_MAX) {                     // the bottom of the range: compare sanitised scores
 #pragma unroll
-    for (int i = 0; i < IPT; ++i) cm |= (sanitize(v[i]) >= tau) ? (kOne << i) : Mask(0);
-  } else {
+      for (int i = 0; i < IPT; ++i) cm |= (sanitize(get(i)) >= tau) ? (kOne << i) : Mask(0);
+    } else {
 #pragma unroll
-    for (int i = 0; i < IPT; ++i) cm |= (v[i] >= tau) ? (kOne << i) : Mask(0);
+      for (int i = 0; i < IPT; ++i) cm |= (get(i) >= tau) ? (kOne << i) : Mask(0);
+    }
+    cm &= content;
   }
-  cm &= content;
   if (cm) {                                    // few threads hold a candidate
     int o = atomicAdd(&L.n, popcnt(cm));
 #pragma unroll
     for (int i = 0; i < IPT; ++i) {
       if ((cm >> i) & kOne) {
-        if (o < kSortCap) L.keys[o] = sel_key(sanitize(v[i]), base + i);
+        if (o < kSortCap) L.keys[o] = sel_key(sanitize(get(i)), base + i);
         ++o;
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   const int n_cand = L.n;
+  on_cand(n_cand);
   if (n_cand <= kSortCap) {
     // rank every candidate against all others, the pairs spread over the workgroup
     if (tid == 0 && (n_cand & 1)) L.keys[n_cand] = 0;   // pad to pairs: key 0 ranks below every key
-    __syncthreads();
+    lds_barrier();
     const int n2 = (n_cand + 1) & ~1;
     const int npad = next_pow2(max(n_cand, 1));
     if (npad <= NT) {
@@ -284,14 +323,12 @@ __device__ void select_content(SelectLds<NT>& L, float (&v)[IPT], MaskT<IPT> con
         L.rank[i] = r;
       }
     }
-    __syncthreads();
+    lds_barrier();
     for (int e = tid; e < n_cand; e += NT)
       if (L.rank[e] < KC) emit(L.rank[e], key_index(L.keys[e]));
     return;
   }
-#pragma unroll
-  for (int i = 0; i < IPT; ++i)
-    if ((content >> i) & kOne) v[i] = sanitize(v[i]);
+  auto sv = [&](int i) { return sanitize(get(i)); };     // the fallback ranks sanitised scores
 
   // ---- fallback: the boundary bin holds too many blocks; refine exactly ----
   Mask cand = content, sel = 0;
@@ -308,7 +345,7 @@ __device__ void select_content(SelectLds<NT>& L, float (&v)[IPT], MaskT<IPT> con
       int o = off;
 #pragma unroll
       for (int i = 0; i < IPT; ++i)
-        if ((cand >> i) & kOne) L.keys[o++] = sel_key(v[i], base + i);
+        if ((cand >> i) & kOne) L.keys[o++] = sel_key(sv(i), base + i);
       const int n = next_pow2(tot);
       for (int i = tot + tid; i < n; i += NT) L.keys[i] = 0;
       __syncthreads();
@@ -316,7 +353,7 @@ __device__ void select_content(SelectLds<NT>& L, float (&v)[IPT], MaskT<IPT> con
       const uint64_t kth = L.keys[need - 1];
 #pragma unroll
       for (int i = 0; i < IPT; ++i)
-        if (((cand >> i) & kOne) && sel_key(v[i], base + i) >= kth) sel |= kOne << i;
+        if (((cand >> i) & kOne) && sel_key(sv(i), base + i) >= kth) sel |= kOne << i;
       nsel += need; need = 0; cand = 0;
       __syncthreads();
       break;
@@ -324,7 +361,7 @@ __device__ void select_content(SelectLds<NT>& L, float (&v)[IPT], MaskT<IPT> con
     float lo2 = FLT_MAX, hi2 = -FLT_MAX;
 #pragma unroll
     for (int i = 0; i < IPT; ++i)
-      if ((cand >> i) & kOne) { lo2 = fminf(lo2, v[i]); hi2 = fmaxf(hi2, v[i]); }
+      if ((cand >> i) & kOne) { lo2 = fminf(lo2, sv(i)); hi2 = fmaxf(hi2, sv(i)); }
     lo2 = block_reduce<NT>(lo2, L.f, OpMin());
     hi2 = block_reduce<NT>(hi2, L.f, OpMax());
     if (lo2 == hi2) {
@@ -346,7 +383,7 @@ __device__ void select_content(SelectLds<NT>& L, float (&v)[IPT], MaskT<IPT> con
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < IPT; ++i)
-      if ((cand >> i) & kOne) atomicAdd(&L.hist[bin2(v[i])], 1);
+      if ((cand >> i) & kOne) atomicAdd(&L.hist[bin2(sv(i))], 1);
     __syncthreads();
     if (tid < kWave) {
       int c4[4], s4 = 0;
@@ -364,7 +401,7 @@ __device__ void select_content(SelectLds<NT>& L, float (&v)[IPT], MaskT<IPT> con
 #pragma unroll
     for (int i = 0; i < IPT; ++i) {
       if ((cand >> i) & kOne) {
-        const int bi = bin2(v[i]);
+        const int bi = bin2(sv(i));
         if (bi < bs2) { sel |= kOne << i; cand &= ~(kOne << i); }
         else if (bi > bs2) cand &= ~(kOne << i);
       }
@@ -380,7 +417,7 @@ __device__ void select_content(SelectLds<NT>& L, float (&v)[IPT], MaskT<IPT> con
     int o = off;
 #pragma unroll
     for (int i = 0; i < IPT; ++i)
-      if ((outm >> i) & kOne) L.keys[o++] = sel_key(v[i], base + i);
+      if ((outm >> i) & kOne) L.keys[o++] = sel_key(sv(i), base + i);
     const int n = next_pow2(tot);
     for (int i = tot + tid; i < n; i += NT) L.keys[i] = 0;
     __syncthreads();
