@@ -26,7 +26,8 @@ ADAKV_ERR_VALUE = 7
 
 ADAKV_F32, ADAKV_F16, ADAKV_BF16 = 0, 1, 2
 POLICY_FIXED, POLICY_ADAPTIVE = 0, 1
-ABI_VERSION = 1
+SUMMARY_CENTROID, SUMMARY_MINMAX = 0, 1
+ABI_VERSION = 2
 
 
 class Geometry(ctypes.Structure):
@@ -51,7 +52,7 @@ class KV(ctypes.Structure):
 
 
 class Centroid(ctypes.Structure):
-    _fields_ = [("data", c_void_p), ("dtype", c_int32)]
+    _fields_ = [("data", c_void_p), ("dtype", c_int32), ("kind", c_int32)]
 
 
 class Budget(ctypes.Structure):

@@ -91,12 +91,17 @@ def instrumentation_active() -> bool:
 
 
 class AdaKVCache:
-    """Full KV cache plus block centroids resident in HBM (adakv/attention.py:106-146).
+    """Full KV cache plus block summaries resident in HBM (adakv/attention.py:106-146).
 
     ``k``/``v`` are ``[n_kv_heads, S, D]`` views of the current length;
-    ``centroid`` is ``[n_kv_heads, n_blocks, D]``.  Decode appends write into
-    preallocated storage and refresh only the trailing block's centroid.
-    ``centroid_dtype`` defaults to the key dtype (fp32 keys: fp32).
+    ``centroid`` is ``[n_kv_heads, n_blocks, D]``.  With ``estimator="minmax"``
+    the cache also holds Quest's per-block key bounds (attention.py:131-138),
+    stored as one ``[n_kv_heads, n_blocks, 2*D]`` buffer of rows [max | min];
+    ``kmax`` and ``kmin`` are ``[n_kv_heads, n_blocks, D]`` views of it.
+    Decode appends write into preallocated storage and refresh only the
+    trailing blocks' summaries.  ``centroid_dtype`` (the summaries' dtype)
+    defaults to the key dtype (fp32 keys: fp32); minmax bounds are kept in
+    the key dtype or fp32, where they are exact.
     """
 
     def __init__(self, block_size: int, estimator: str = "centroid", centroid_dtype=None):
@@ -107,11 +112,10 @@ class AdaKVCache:
         self.centroid_dtype = centroid_dtype
         self.k = None
         self.v = None
-        self.kmin = None
-        self.kmax = None
         self._kbuf = None
         self._vbuf = None
         self._cbuf = None          # [1, Hkv, capacity_blocks, D]
+        self._mbuf = None          # [1, Hkv, capacity_blocks, 2*D] (minmax only)
 
     @property
     def seq_len(self) -> int:
@@ -127,13 +131,32 @@ class AdaKVCache:
             return None
         return self._cbuf[0, :, : self.n_blocks]
 
-    def _require_centroid(self):
-        if self.estimator == "minmax":
-            raise NotImplementedError("the minmax (Quest) estimator has no HIP kernel yet")
+    @property
+    def kmax(self):
+        """Per-block per-dimension key maxima [Hkv, n_blocks, D] (minmax caches)."""
+        if self._mbuf is None:
+            return None
+        return self._mbuf[0, :, : self.n_blocks, : self._mbuf.shape[3] // 2]
+
+    @property
+    def kmin(self):
+        """Per-block per-dimension key minima [Hkv, n_blocks, D] (minmax caches)."""
+        if self._mbuf is None:
+            return None
+        return self._mbuf[0, :, : self.n_blocks, self._mbuf.shape[3] // 2:]
+
+    def summary(self, estimator: str):
+        """The [1, Hkv, capacity_blocks, row] summary buffer an estimator scores."""
+        if estimator == "minmax":
+            if self._mbuf is None:
+                raise ValueError("minmax estimator needs AdaKVCache(estimator='minmax')")
+            return self._mbuf
+        if estimator != "centroid":
+            raise ValueError(f"unknown estimator: {estimator!r}")
+        return self._cbuf
 
     def append_prefill(self, k, v):
-        """Store the prefill KV and build every block centroid. k, v: [Hkv, S, D]."""
-        self._require_centroid()
+        """Store the prefill KV and build every block summary. k, v: [Hkv, S, D]."""
         self.k, self.v = k, v
         self._kbuf = self._vbuf = None
         Hkv, S, D = k.shape
@@ -142,7 +165,21 @@ class AdaKVCache:
         cap = nb + max(64, nb // 8)
         self._cbuf = torch.zeros(1, Hkv, cap, D, dtype=cdt, device=k.device)
         ops.centroid_build(k.unsqueeze(0), self.block_size, centroid=self._cbuf)
+        self._mbuf = None
+        if self.estimator == "minmax":
+            mdt = cdt if cdt in (k.dtype, torch.float32) else torch.float32
+            self._mbuf = torch.zeros(1, Hkv, cap, 2 * D, dtype=mdt, device=k.device)
+            ops.centroid_build(k.unsqueeze(0), self.block_size, centroid=self._mbuf)
         return self
+
+    @staticmethod
+    def _grown(buf, nb):
+        if nb <= buf.shape[2]:
+            return buf
+        grown = torch.zeros(1, buf.shape[1], nb + max(64, nb // 8), buf.shape[3], dtype=buf.dtype,
+                            device=buf.device)
+        grown[:, :, : buf.shape[2]].copy_(buf)
+        return grown
 
     def _grow_kv(self, need: int):
         Hkv, S, D = self.k.shape
@@ -155,8 +192,7 @@ class AdaKVCache:
 
     def append_decode(self, k_t, v_t):
         """Append decoded tokens' KV (k_t, v_t: [Hkv, n, D]) and refresh the
-        affected centroids in O(block_size * D) per KV head (adakv/runtime.py:43-60)."""
-        self._require_centroid()
+        affected summaries in O(block_size * D) per KV head (adakv/runtime.py:43-60)."""
         S, n = self.seq_len, int(k_t.shape[1])
         if self._kbuf is None or S + n > self._kbuf.shape[1]:
             self._grow_kv(S + n)
@@ -165,12 +201,11 @@ class AdaKVCache:
         self.k = self._kbuf[:, : S + n]
         self.v = self._vbuf[:, : S + n]
         nb = ops.n_blocks(S + n, self.block_size)
-        if nb > self._cbuf.shape[2]:
-            grown = torch.zeros(1, self._cbuf.shape[1], nb + max(64, nb // 8), self._cbuf.shape[3],
-                                dtype=self._cbuf.dtype, device=self._cbuf.device)
-            grown[:, :, : self._cbuf.shape[2]].copy_(self._cbuf)
-            self._cbuf = grown
+        self._cbuf = self._grown(self._cbuf, nb)
         ops.centroid_append(self.k.unsqueeze(0), self._cbuf, self.block_size, n_new=n)
+        if self._mbuf is not None:
+            self._mbuf = self._grown(self._mbuf, nb)
+            ops.centroid_append(self.k.unsqueeze(0), self._mbuf, self.block_size, n_new=n)
         return self
 
 
@@ -182,14 +217,14 @@ def _budget(avg_budget, k_min, k_max, n_sink_blocks, n_local_blocks, temperature
 
 
 def _validate(cache, estimator, budget_policy):
-    if estimator == "minmax":
-        if cache.kmin is None or cache.kmax is None:
-            raise ValueError("minmax estimator needs AdaKVCache(estimator='minmax')")
-        raise NotImplementedError("the minmax (Quest) estimator has no HIP kernel yet")
-    if estimator != "centroid":
+    """The summary buffer the estimator scores (adakv/attention.py:185-198 errors)."""
+    if estimator == "minmax" and (cache.kmin is None or cache.kmax is None):
+        raise ValueError("minmax estimator needs AdaKVCache(estimator='minmax')")
+    if estimator not in ("centroid", "minmax"):
         raise ValueError(f"unknown estimator: {estimator!r}")
     if budget_policy not in ("fixed", "adaptive", "adaptive_nucleus"):
         raise ValueError(f"unknown budget_policy: {budget_policy!r}")
+    return cache.summary(estimator)
 
 
 def plan_selection(q, cache: AdaKVCache, avg_budget, k_min: int = 2, k_max: int = 64,
@@ -202,11 +237,11 @@ def plan_selection(q, cache: AdaKVCache, avg_budget, k_min: int = 2, k_max: int 
     Returns (block_table int32 [Hq, T], sel_lens int32 [Hq]); rows hold the
     forced sink/local blocks, then content blocks by descending score.
     """
-    _validate(cache, estimator, budget_policy)
+    summ = _validate(cache, estimator, budget_policy)
     budget = _budget(avg_budget, k_min, k_max, n_sink_blocks, n_local_blocks, temperature,
                      budget_policy, c_min)
-    table, lens = ops.plan(q.unsqueeze(0), cache._cbuf, cache.block_size, budget,
-                           seq_len=cache.seq_len)
+    table, lens = ops.plan(q.unsqueeze(0), summ, cache.block_size, budget,
+                           seq_len=cache.seq_len, estimator=estimator)
     block_table, sel_lens = table[0], lens[0]
     record_selection(block_table, sel_lens, cache.n_blocks)
     return block_table, sel_lens
@@ -218,13 +253,13 @@ def adakv_decode_attention(q, cache: AdaKVCache, avg_budget, k_min: int = 2, k_m
                            budget_policy: str = "adaptive", c_min: int = 1):
     """One AdaKV decode step: plan + sparse decode in one C call (three
     kernels, no host sync).  q: [Hq, D] -> [Hq, D] (adakv/attention.py:250-268)."""
-    _validate(cache, estimator, budget_policy)
+    summ = _validate(cache, estimator, budget_policy)
     budget = _budget(avg_budget, k_min, k_max, n_sink_blocks, n_local_blocks, temperature,
                      budget_policy, c_min)
     D = q.shape[-1]
-    res = ops.decode_fused(q.unsqueeze(0), cache.k.unsqueeze(0), cache.v.unsqueeze(0), cache._cbuf,
+    res = ops.decode_fused(q.unsqueeze(0), cache.k.unsqueeze(0), cache.v.unsqueeze(0), summ,
                            cache.block_size, budget, sm_scale=1.0 / math.sqrt(D),
-                           return_selection=instrumentation_active())
+                           return_selection=instrumentation_active(), estimator=estimator)
     if instrumentation_active():
         out, table, lens = res
         record_selection(table[0], lens[0], cache.n_blocks)

@@ -32,12 +32,18 @@ int per_vec(int dt) { return 16 / elt_bytes(dt); }
 int gmax_of(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8; }
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Centroid element type per key element type: the key type itself or fp32
-// (fp32 keys may also be summarised in bf16).
-bool centroid_pair_ok(int kdt, int cdt) {
-  if (cdt == ADAKV_F32) return true;
-  if (kdt == ADAKV_F32) return cdt == ADAKV_BF16;
-  return kdt == cdt;
+// Summary element type per key element type: the key type itself or fp32;
+// fp32 keys may also have bf16 centroids (a rounded mean), but minmax rows
+// are kept exact (a rounded max or min would no longer bound the keys).
+bool centroid_pair_ok(int kdt, const adakv_centroid_t* c) {
+  if (c->dtype == ADAKV_F32) return true;
+  if (kdt == ADAKV_F32) return c->kind == ADAKV_SUMMARY_CENTROID && c->dtype == ADAKV_BF16;
+  return kdt == c->dtype;
+}
+
+// Elements per summary row: head_dim (centroid) or 2 * head_dim (minmax).
+int row_len(const adakv_geometry_t* g, const adakv_centroid_t* c) {
+  return c->kind == ADAKV_SUMMARY_MINMAX ? 2 * g->head_dim : g->head_dim;
 }
 
 int check_geometry(const adakv_geometry_t* g) {
@@ -79,9 +85,11 @@ int check_out(const adakv_output_t* o) {
   return ADAKV_OK;
 }
 
-int check_centroid(const adakv_centroid_t* c) {
+int check_centroid(const adakv_geometry_t* g, const adakv_centroid_t* c) {
   if (!c || !c->data) return ADAKV_ERR_NULL;
   if (!valid_dtype(c->dtype)) return ADAKV_ERR_DTYPE;
+  if (c->kind != ADAKV_SUMMARY_CENTROID && c->kind != ADAKV_SUMMARY_MINMAX) return ADAKV_ERR_VALUE;
+  if (c->kind == ADAKV_SUMMARY_MINMAX && g->head_dim > 128) return ADAKV_ERR_UNSUPPORTED;
   if (!aligned16(c->data)) return ADAKV_ERR_VALUE;
   return ADAKV_OK;
 }
@@ -144,6 +152,11 @@ BudgetCfg budget_cfg(const adakv_budget_t* p) {
 
 int status_of(hipError_t e) { return e == hipSuccess ? ADAKV_OK : ADAKV_ERR_LAUNCH; }
 
+hipError_t run_summary(const CentroidArgs& a, int kdt, const adakv_centroid_t* c, int D, hipStream_t s) {
+  if (c->kind == ADAKV_SUMMARY_MINMAX) return launch_minmax(a, kdt, c->dtype, D, s);
+  return launch_centroid(a, kdt, c->dtype, D, s);
+}
+
 CentroidArgs centroid_args(const adakv_geometry_t* g, const adakv_kv_t* kv, const int32_t* lens,
                            const adakv_centroid_t* c, int n_new) {
   CentroidArgs a{};
@@ -167,6 +180,7 @@ ScoreArgs score_args(const adakv_geometry_t* g, const adakv_query_t* q, const ad
   sa.scores = scores; sa.sp = sp;
   sa.q_vec = q->dtype == c->dtype && q->dtype != ADAKV_F32 && aligned16(q->data) && q->stride_b % 8 == 0 &&
              q->stride_h % 8 == 0;
+  sa.minmax = c->kind == ADAKV_SUMMARY_MINMAX;
   return sa;
 }
 
@@ -185,7 +199,7 @@ int run_scores(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_ce
   sa.parts = reinterpret_cast<float*>(ws + L.parts);
   sa.parts_pitch = L.parts_pitch;
   sa.cfg = budget_cfg(p);
-  if (launch_score(sa, c->dtype, g->head_dim, s) != hipSuccess) return ADAKV_ERR_LAUNCH;
+  if (launch_score(sa, c->dtype, row_len(g, c), s) != hipSuccess) return ADAKV_ERR_LAUNCH;
   SelectArgs& se = *se_out;
   se = SelectArgs{};
   se.scores = sa.scores; se.sp = L.sp;
@@ -316,7 +330,8 @@ WorkspaceLayout workspace_layout(const adakv_geometry_t& g, int T) {
   off = align_up(off + (size_t)g.batch * g.n_kv_heads * L.nsplit_max * G * (g.head_dim + 2) * 4);
   L.table = off;         off = align_up(off + (size_t)g.batch * g.n_q_heads * T * 4);
   L.lens = off;          off = align_up(off + (size_t)g.batch * g.n_q_heads * 4);
-  L.parts_pitch = score_chunks_max(g.max_blocks, g.head_dim);
+  // records per row for either summary kind (a minmax row is 2 * head_dim long)
+  L.parts_pitch = score_chunks_max(g.max_blocks, std::min(2 * g.head_dim, 256));
   L.parts = off;
   off = align_up(off + (size_t)g.batch * g.n_q_heads * L.parts_pitch * kPartFloats * 4);
   L.total = off;
@@ -358,37 +373,37 @@ size_t adakv_workspace_bytes(const adakv_geometry_t* g, int32_t table_width) {
 int adakv_centroid_build(const adakv_geometry_t* g, const adakv_kv_t* kv, const int32_t* seq_lens,
                          const adakv_centroid_t* c, void* stream) {
   int st;
-  if ((st = check_geometry(g)) || (st = check_kv(g, kv, false)) || (st = check_centroid(c))) return st;
-  if (!centroid_pair_ok(kv->dtype, c->dtype)) return ADAKV_ERR_DTYPE;
+  if ((st = check_geometry(g)) || (st = check_kv(g, kv, false)) || (st = check_centroid(g, c))) return st;
+  if (!centroid_pair_ok(kv->dtype, c)) return ADAKV_ERR_DTYPE;
   CentroidArgs a = centroid_args(g, kv, seq_lens, c, 0);
-  return status_of(launch_centroid(a, kv->dtype, c->dtype, g->head_dim, (hipStream_t)stream));
+  return status_of(run_summary(a, kv->dtype, c, g->head_dim, (hipStream_t)stream));
 }
 
 int adakv_centroid_append(const adakv_geometry_t* g, const adakv_kv_t* kv, const int32_t* seq_lens,
                           int32_t n_new, const adakv_centroid_t* c, void* stream) {
   int st;
-  if ((st = check_geometry(g)) || (st = check_kv(g, kv, false)) || (st = check_centroid(c))) return st;
+  if ((st = check_geometry(g)) || (st = check_kv(g, kv, false)) || (st = check_centroid(g, c))) return st;
   if (n_new < 1 || n_new > g->max_seq_len) return ADAKV_ERR_VALUE;
-  if (!centroid_pair_ok(kv->dtype, c->dtype)) return ADAKV_ERR_DTYPE;
+  if (!centroid_pair_ok(kv->dtype, c)) return ADAKV_ERR_DTYPE;
   CentroidArgs a = centroid_args(g, kv, seq_lens, c, n_new);
-  return status_of(launch_centroid(a, kv->dtype, c->dtype, g->head_dim, (hipStream_t)stream));
+  return status_of(run_summary(a, kv->dtype, c, g->head_dim, (hipStream_t)stream));
 }
 
 int adakv_block_scores(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_centroid_t* c,
                        const int32_t* seq_lens, float* scores, int32_t pitch, void* stream) {
   int st;
-  if ((st = check_geometry(g)) || (st = check_q(q)) || (st = check_centroid(c))) return st;
+  if ((st = check_geometry(g)) || (st = check_q(q)) || (st = check_centroid(g, c))) return st;
   if (!scores) return ADAKV_ERR_NULL;
   if (pitch < g->max_blocks) return ADAKV_ERR_SHAPE;
   ScoreArgs sa = score_args(g, q, c, seq_lens, scores, pitch);
-  return status_of(launch_score(sa, c->dtype, g->head_dim, (hipStream_t)stream));
+  return status_of(launch_score(sa, c->dtype, row_len(g, c), (hipStream_t)stream));
 }
 
 int adakv_plan(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_centroid_t* c,
                const int32_t* seq_lens, const adakv_budget_t* p, const adakv_selection_t* sel,
                void* ws, size_t ws_bytes, void* stream) {
   int st;
-  if ((st = check_geometry(g)) || (st = check_q(q)) || (st = check_centroid(c)) ||
+  if ((st = check_geometry(g)) || (st = check_q(q)) || (st = check_centroid(g, c)) ||
       (st = check_budget(p)))
     return st;
   if (!sel || !sel->block_table || !sel->sel_lens) return ADAKV_ERR_NULL;
@@ -422,7 +437,7 @@ int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const 
                        void* stream) {
   int st;
   if ((st = check_geometry(g)) || (st = check_q(q)) || (st = check_kv(g, kv, true)) ||
-      (st = check_centroid(c)) || (st = check_budget(p)) || (st = check_out(out)))
+      (st = check_centroid(g, c)) || (st = check_budget(p)) || (st = check_out(out)))
     return st;
   if (append_new < 0 || append_new > g->max_seq_len) return ADAKV_ERR_VALUE;
   if (!isfinite(sm_scale)) return ADAKV_ERR_VALUE;
@@ -439,7 +454,7 @@ int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const 
   int32_t* table = sel ? sel->block_table : reinterpret_cast<int32_t*>(w + L.table);
   int32_t* lens = sel ? sel->sel_lens : reinterpret_cast<int32_t*>(w + L.lens);
   const hipStream_t s = (hipStream_t)stream;
-  if (append_new > 0 && !centroid_pair_ok(kv->dtype, c->dtype)) return ADAKV_ERR_DTYPE;
+  if (append_new > 0 && !centroid_pair_ok(kv->dtype, c)) return ADAKV_ERR_DTYPE;
   // bf16 / fp16 K/V (and q of the same type, 16-byte aligned rows) on a shape the fused kernel
   // serves: scores, then one kernel for the budget, the selection and the
   // decode of every head

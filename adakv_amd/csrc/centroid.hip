@@ -1,15 +1,20 @@
-// Block-centroid kernels: mean key of each block_size-token block over its
-// real tokens (adakv/estimator.py:27-48, adakv/attention.py:119-139).
+// Block-summary kernels over each block_size-token block's real tokens:
 //
-// Each lane owns one 16-byte slice of head_dim for one block and adds the
-// block's tokens in order, in fp32, then divides once by the token count with
-// IEEE round-to-nearest.  That is the same operation sequence as NumPy's
-// keys[:, s:e].mean(axis=1) on fp32 data, so fp32 centroids are bit-identical
-// to the oracle; bf16 / fp16 centroids are that value rounded once.
+// * centroid: the mean key (adakv/estimator.py:27-48, adakv/attention.py:119-139).
+//   Each lane owns one 16-byte slice of head_dim for one block and adds the
+//   block's tokens in order, in fp32, then divides once by the token count
+//   with IEEE round-to-nearest.  That is the same operation sequence as
+//   NumPy's keys[:, s:e].mean(axis=1) on fp32 data, so fp32 centroids are
+//   bit-identical to the oracle; bf16 / fp16 centroids are that value rounded
+//   once.
+// * minmax: the per-dimension max and min of the keys (Quest's block bounds,
+//   adakv/estimator.py:50-57, adakv/attention.py:131-138), stored as one row
+//   of 2*head_dim elements, [max | min].  Both are exact in the key type and
+//   in fp32, so they are bit-identical to the oracle whatever the order.
 //
 // Append mode recomputes only the blocks that hold the newest n_new tokens.
-// Because the sum restarts from the block's first token, an appended centroid
-// has the same bits as a full rebuild (the reference's running mean,
+// Because the reduction restarts from the block's first token, an appended
+// summary has the same bits as a full rebuild (the reference's running mean,
 // adakv/runtime.py:52-59, drifts by rounding instead).
 #include "common.hpp"
 #include "internal.hpp"
@@ -40,7 +45,7 @@ __device__ __forceinline__ void store_row(void* base, int64_t off, const float* 
   }
 }
 
-template <int KDT, int CDT, int D>
+template <int KDT, int CDT, int D, bool MM>
 __global__ __launch_bounds__(256) void centroid_kernel(CentroidArgs a) {
   constexpr int EPV = Elt<KDT>::kPerVec;
   constexpr int EB = Elt<KDT>::kBytes;
@@ -60,7 +65,7 @@ __global__ __launch_bounds__(256) void centroid_kernel(CentroidArgs a) {
   const char* kp = reinterpret_cast<const char*>(a.k) +
                    ((int64_t)b * a.sb + (int64_t)kvh * a.sh + (int64_t)t0 * a.ss + seg * EPV) * EB;
   const int64_t step = a.ss * EB;
-  float acc[EPV];
+  float acc[EPV], lo[EPV];
   for (int t = t0; t < t1; t += U) {
     uint4 raw[U];
 #pragma unroll
@@ -72,18 +77,32 @@ __global__ __launch_bounds__(256) void centroid_kernel(CentroidArgs a) {
         float x[EPV];
         unpack<KDT>(raw[u], x);
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) acc[e] = (t + u == t0) ? x[e] : acc[e] + x[e];
+        for (int e = 0; e < EPV; ++e) {
+          if constexpr (MM) {
+            acc[e] = (t + u == t0) ? x[e] : fmaxf(acc[e], x[e]);
+            lo[e] = (t + u == t0) ? x[e] : fminf(lo[e], x[e]);
+          } else {
+            acc[e] = (t + u == t0) ? x[e] : acc[e] + x[e];
+          }
+        }
       }
     }
   }
-  const float cnt = (float)(t1 - t0);
+  if constexpr (MM) {
+    // row of 2*D elements: the maxima, then the minima
+    const int64_t row = (((int64_t)b * a.Hkv + kvh) * a.max_blocks + blk) * (2 * D) + seg * EPV;
+    store_row<CDT, EPV>(a.c, row, acc);
+    store_row<CDT, EPV>(a.c, row + D, lo);
+  } else {
+    const float cnt = (float)(t1 - t0);
 #pragma unroll
-  for (int e = 0; e < EPV; ++e) acc[e] = __fdiv_rn(acc[e], cnt);
-  const int64_t row = (((int64_t)b * a.Hkv + kvh) * a.max_blocks + blk) * D + seg * EPV;
-  store_row<CDT, EPV>(a.c, row, acc);
+    for (int e = 0; e < EPV; ++e) acc[e] = __fdiv_rn(acc[e], cnt);
+    const int64_t row = (((int64_t)b * a.Hkv + kvh) * a.max_blocks + blk) * D + seg * EPV;
+    store_row<CDT, EPV>(a.c, row, acc);
+  }
 }
 
-template <int KDT, int CDT>
+template <int KDT, int CDT, bool MM>
 hipError_t launch_d(const CentroidArgs& a, int D, hipStream_t s) {
   auto go = [&](auto kern, int bpw) {
     int span = a.max_blocks;
@@ -94,10 +113,10 @@ hipError_t launch_d(const CentroidArgs& a, int D, hipStream_t s) {
   };
   constexpr int EPV = Elt<KDT>::kPerVec;
   switch (D) {
-    case 32: return go(centroid_kernel<KDT, CDT, 32>, 4 * (kWave / (32 / EPV)));
-    case 64: return go(centroid_kernel<KDT, CDT, 64>, 4 * (kWave / (64 / EPV)));
-    case 128: return go(centroid_kernel<KDT, CDT, 128>, 4 * (kWave / (128 / EPV)));
-    case 256: return go(centroid_kernel<KDT, CDT, 256>, 4 * (kWave / (256 / EPV)));
+    case 32: return go(centroid_kernel<KDT, CDT, 32, MM>, 4 * (kWave / (32 / EPV)));
+    case 64: return go(centroid_kernel<KDT, CDT, 64, MM>, 4 * (kWave / (64 / EPV)));
+    case 128: return go(centroid_kernel<KDT, CDT, 128, MM>, 4 * (kWave / (128 / EPV)));
+    case 256: return go(centroid_kernel<KDT, CDT, 256, MM>, 4 * (kWave / (256 / EPV)));
     default: return hipErrorInvalidValue;
   }
 }
@@ -105,10 +124,20 @@ hipError_t launch_d(const CentroidArgs& a, int D, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_centroid(const CentroidArgs& a, int kdt, int cdt, int D, hipStream_t s) {
-#define ADAKV_C(K, C) if (kdt == K && cdt == C) return launch_d<K, C>(a, D, s);
+#define ADAKV_C(K, C) if (kdt == K && cdt == C) return launch_d<K, C, false>(a, D, s);
   ADAKV_C(ADAKV_BF16, ADAKV_BF16) ADAKV_C(ADAKV_BF16, ADAKV_F32)
   ADAKV_C(ADAKV_F16, ADAKV_F16) ADAKV_C(ADAKV_F16, ADAKV_F32)
   ADAKV_C(ADAKV_F32, ADAKV_F32) ADAKV_C(ADAKV_F32, ADAKV_BF16)
+#undef ADAKV_C
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_minmax(const CentroidArgs& a, int kdt, int cdt, int D, hipStream_t s) {
+  if (D > 128) return hipErrorInvalidValue;
+#define ADAKV_C(K, C) if (kdt == K && cdt == C) return launch_d<K, C, true>(a, D, s);
+  ADAKV_C(ADAKV_BF16, ADAKV_BF16) ADAKV_C(ADAKV_BF16, ADAKV_F32)
+  ADAKV_C(ADAKV_F16, ADAKV_F16) ADAKV_C(ADAKV_F16, ADAKV_F32)
+  ADAKV_C(ADAKV_F32, ADAKV_F32)
 #undef ADAKV_C
   return hipErrorInvalidValue;
 }

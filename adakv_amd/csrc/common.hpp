@@ -87,22 +87,27 @@ __device__ __forceinline__ void with_dtype(int dt, F&& f) {
 
 // Rows [G][D] of q (row g at element base + g * qsh) into LDS as fp32 times
 // `scale`; all loads of a thread are issued before the first is consumed.
-template <int NT, int GMAX, int D>
+// SPLIT: the rows are [max(q, 0) | min(q, 0)] of q rows of D/2 elements (the
+// query side of a minmax block summary).
+template <int NT, int GMAX, int D, bool SPLIT = false>
 __device__ __forceinline__ void stage_q(float (*s_q)[D], const void* q, int qdt, int64_t base, int64_t qsh,
                                         int G, float scale) {
   constexpr int IT = (GMAX * D + NT - 1) / NT;
+  constexpr int DQ = SPLIT ? D / 2 : D;
   with_dtype(qdt, [&](auto tag) {
     constexpr int DT = decltype(tag)::value;
     float x[IT];
 #pragma unroll
     for (int u = 0; u < IT; ++u) {
       const int i = min((int)threadIdx.x + u * NT, G * D - 1);     // in-bounds for every lane
-      x[u] = load_t<DT>(q, base + (int64_t)(i / D) * qsh + i % D);
+      x[u] = load_t<DT>(q, base + (int64_t)(i / D) * qsh + (i % D) % DQ);
     }
 #pragma unroll
     for (int u = 0; u < IT; ++u) {
       const int i = threadIdx.x + u * NT;
-      if (i < G * D) s_q[i / D][i % D] = x[u] * scale;
+      float y = x[u];
+      if constexpr (SPLIT) y = (i % D) < DQ ? fmaxf(y, 0.f) : fminf(y, 0.f);
+      if (i < G * D) s_q[i / D][i % D] = y * scale;
     }
   });
 }

@@ -14,7 +14,7 @@ namespace adakv {
 struct CentroidArgs {
   const void* k;
   int64_t sb, sh, ss;          // K strides (elements)
-  void* c;                     // [B, Hkv, max_blocks, D]
+  void* c;                     // [B, Hkv, max_blocks, D] (minmax: [..., 2 * D])
   const int32_t* seq_lens;
   int uniform_len;
   int B, Hkv, bs, max_blocks;
@@ -43,7 +43,8 @@ struct ScoreArgs {
   int parts_pitch;
   BudgetCfg cfg;
   int n_app, n_chunks, chunk_rows;   // set by the launcher
-  int q_vec;                   // 1: q has the centroid type and 16-byte aligned rows (vector loads)
+  int q_vec;                   // 1: q has the summary type and 16-byte aligned rows (vector loads)
+  int minmax;                  // 1: rows are minmax summaries [max | min] of 2*head_dim elements
 };
 
 // Softmax record of a score workgroup's rows for one head (z = score /
@@ -138,8 +139,12 @@ struct WorkspaceLayout {
 WorkspaceLayout workspace_layout(const adakv_geometry_t& g, int table_width);
 
 hipError_t launch_centroid(const CentroidArgs& a, int kdt, int cdt, int D, hipStream_t s);
-// Sets a.n_app, a.n_chunks and a.chunk_rows for the chosen kernel.
+// Per-dimension max and min of every block's keys, rows [max | min] (D <= 128).
+hipError_t launch_minmax(const CentroidArgs& a, int kdt, int cdt, int D, hipStream_t s);
+// Sets a.n_app, a.n_chunks and a.chunk_rows for the chosen kernel.  D: the
+// summary row length (head_dim, or 2 * head_dim when a.minmax).
 hipError_t launch_score(ScoreArgs& a, int cdt, int D, hipStream_t s);
+hipError_t launch_score_minmax(ScoreArgs& a, int cdt, int D, hipStream_t s);
 // Chunks per (sequence, KV head) for any centroid dtype: bound on parts_pitch.
 int score_chunks_max(int max_blocks, int D);
 hipError_t launch_select(const SelectArgs& a, int max_blocks, hipStream_t s);

@@ -6,7 +6,11 @@ in the HIP kernels.  Tensors must live on a ROCm device: there is no CPU path.
 Layouts (head_dim contiguous, any other strides):
     q         [B, Hq, D]
     k, v      [B, Hkv, S, D]          (k and v share one stride set)
-    centroid  [B, Hkv, max_blocks, D] (contiguous)
+    centroid  [B, Hkv, max_blocks, D] (contiguous) -- or, for the minmax (Quest)
+              estimator, [B, Hkv, max_blocks, 2*D]: per block the per-dimension
+              max of its keys, then their min.  Every op that takes a summary
+              reads its kind from its last dimension (D or 2*D); ``estimator=``
+              states it explicitly.
     table     [B, Hq, T] int32, sel_lens [B, Hq] int32
     seq_lens  [B] int32 on the device, or None (= every sequence holds S tokens)
 """
@@ -124,10 +128,31 @@ def _kv(k: torch.Tensor, v: torch.Tensor | None) -> C.KV:
                 k.stride(0), k.stride(1), k.stride(2))
 
 
-def _centroid(c: torch.Tensor) -> C.Centroid:
+_ESTIMATORS = {"centroid": C.SUMMARY_CENTROID, "minmax": C.SUMMARY_MINMAX}
+
+
+def summary_kind(c: torch.Tensor, head_dim: int, estimator: str | None = None) -> str:
+    """The estimator a summary tensor serves: its last dimension is head_dim
+    (centroid) or 2 * head_dim (minmax); ``estimator`` must agree when given."""
+    if estimator is not None and estimator not in _ESTIMATORS:
+        raise ValueError(f"unknown estimator: {estimator!r}")
+    last = c.shape[-1]
+    kind = "centroid" if last == head_dim else "minmax" if last == 2 * head_dim else None
+    if kind is None:
+        raise ValueError(f"summary rows hold {last} elements; expected head_dim ({head_dim}) for "
+                         f"centroids or 2*head_dim ({2 * head_dim}) for minmax bounds")
+    if estimator is not None and estimator != kind:
+        if estimator == "minmax":
+            raise ValueError("minmax estimator needs minmax summaries [.., 2*head_dim] "
+                             "(AdaKVCache(estimator='minmax'))")
+        raise ValueError(f"estimator {estimator!r} does not match {kind} summaries")
+    return kind
+
+
+def _centroid(c: torch.Tensor, head_dim: int, estimator: str | None = None) -> C.Centroid:
     if c.dim() != 4 or not c.is_contiguous():
-        raise ValueError("centroid must be a contiguous [B, Hkv, max_blocks, D] tensor")
-    return C.Centroid(c.data_ptr(), _dt(c))
+        raise ValueError("centroid must be a contiguous [B, Hkv, max_blocks, D or 2*D] tensor")
+    return C.Centroid(c.data_ptr(), _dt(c), _ESTIMATORS[summary_kind(c, head_dim, estimator)])
 
 
 def geometry(B, Hq, Hkv, D, block_size, max_seq_len, max_blocks) -> C.Geometry:
@@ -151,41 +176,50 @@ def n_blocks(seq_len: int, block_size: int) -> int:
 
 # ---------------------------------------------------------------------------
 def centroid_build(k: torch.Tensor, block_size: int, seq_lens=None, centroid=None,
-                   centroid_dtype=None, max_blocks=None) -> torch.Tensor:
-    """Block centroids of k [B, Hkv, S, D] -> [B, Hkv, max_blocks, D]
-    (adakv/estimator.py:27-48).  Rows past a sequence's last block are left as
-    they were (zeros for a new tensor)."""
+                   centroid_dtype=None, max_blocks=None, estimator: str | None = None) -> torch.Tensor:
+    """Block summaries of k [B, Hkv, S, D]: centroids [B, Hkv, max_blocks, D]
+    (adakv/estimator.py:27-48) or, with ``estimator="minmax"`` (or a given
+    ``centroid`` tensor of rows 2*D), the per-dimension [max | min] bounds
+    [B, Hkv, max_blocks, 2*D] (adakv/estimator.py:50-57).  Rows past a
+    sequence's last block are left as they were (zeros for a new tensor)."""
     dev = _on_device(k, centroid, seq_lens)
     B, Hkv, S, D = k.shape
     nb = n_blocks(S, block_size)
     if centroid is None:
+        est = estimator or "centroid"
+        if est not in _ESTIMATORS:
+            raise ValueError(f"unknown estimator kind: {est!r}")
         cdt = centroid_dtype or (torch.float32 if k.dtype == torch.float32 else k.dtype)
-        centroid = torch.zeros(B, Hkv, max(max_blocks or nb, nb), D, dtype=cdt, device=dev)
+        row = 2 * D if est == "minmax" else D
+        centroid = torch.zeros(B, Hkv, max(max_blocks or nb, nb), row, dtype=cdt, device=dev)
     g = geometry(B, Hkv, Hkv, D, block_size, S, centroid.shape[2])
     C.check(C.load().adakv_centroid_build(ctypes.byref(g), ctypes.byref(_kv(k, None)),
                                           _ptr(_seq_lens(seq_lens, dev)),
-                                          ctypes.byref(_centroid(centroid)), _stream(dev)),
+                                          ctypes.byref(_centroid(centroid, D, estimator)), _stream(dev)),
             "centroid_build")
     return centroid
 
 
 def centroid_append(k: torch.Tensor, centroid: torch.Tensor, block_size: int, n_new: int = 1,
                     seq_lens=None) -> torch.Tensor:
-    """Refresh, in place, the centroids of the blocks holding the newest
-    ``n_new`` tokens of every sequence (adakv/runtime.py:43-60)."""
+    """Refresh, in place, the summaries (centroids or minmax bounds) of the
+    blocks holding the newest ``n_new`` tokens of every sequence
+    (adakv/runtime.py:43-60)."""
     dev = _on_device(k, centroid, seq_lens)
     B, Hkv, S, D = k.shape
     g = geometry(B, Hkv, Hkv, D, block_size, S, centroid.shape[2])
     C.check(C.load().adakv_centroid_append(ctypes.byref(g), ctypes.byref(_kv(k, None)),
                                            _ptr(_seq_lens(seq_lens, dev)), int(n_new),
-                                           ctypes.byref(_centroid(centroid)), _stream(dev)),
+                                           ctypes.byref(_centroid(centroid, D)), _stream(dev)),
             "centroid_append")
     return centroid
 
 
 def block_scores(q: torch.Tensor, centroid: torch.Tensor, block_size: int, seq_len=None,
-                 seq_lens=None, out=None) -> torch.Tensor:
-    """q . centroid for every block, fp32 [B, Hq, max_blocks] (adakv/estimator.py:62-74)."""
+                 seq_lens=None, out=None, estimator: str | None = None) -> torch.Tensor:
+    """Score of every block, fp32 [B, Hq, max_blocks]: q . centroid
+    (adakv/estimator.py:62-74) or, for minmax summaries, the Quest bound
+    max(q,0) . kmax + min(q,0) . kmin (adakv/estimator.py:76-79)."""
     dev = _on_device(q, centroid, seq_lens, out)
     B, Hq, D = q.shape
     _, Hkv, maxb, _ = centroid.shape
@@ -196,7 +230,7 @@ def block_scores(q: torch.Tensor, centroid: torch.Tensor, block_size: int, seq_l
     if out.dtype != torch.float32 or not out.is_contiguous() or out.shape[:2] != (B, Hq):
         raise ValueError("scores must be a contiguous fp32 [B, Hq, pitch] tensor")
     C.check(C.load().adakv_block_scores(ctypes.byref(g), ctypes.byref(_q(q)),
-                                        ctypes.byref(_centroid(centroid)),
+                                        ctypes.byref(_centroid(centroid, D, estimator)),
                                         _ptr(_seq_lens(seq_lens, dev)), _ptr(out), out.shape[2],
                                         _stream(dev)), "block_scores")
     return out
@@ -211,7 +245,8 @@ def table_width(B, Hq, Hkv, D, block_size, max_seq_len, max_blocks, budget: Budg
 
 
 def plan(q: torch.Tensor, centroid: torch.Tensor, block_size: int, budget: BudgetParams,
-         seq_len: int | None = None, seq_lens=None, table=None, sel_lens=None):
+         seq_len: int | None = None, seq_lens=None, table=None, sel_lens=None,
+         estimator: str | None = None):
     """Scores + budget + selection (adakv/attention.py:149-247).
 
     Returns (table [B, Hq, T] int32, sel_lens [B, Hq] int32); the first
@@ -236,7 +271,8 @@ def plan(q: torch.Tensor, centroid: torch.Tensor, block_size: int, budget: Budge
     nbytes = C.load().adakv_workspace_bytes(ctypes.byref(g), table.shape[-1])
     ws = workspace(dev, nbytes)
     sel = C.Selection(table.data_ptr(), table.shape[-1], sel_lens.data_ptr())
-    C.check(C.load().adakv_plan(ctypes.byref(g), ctypes.byref(_q(q)), ctypes.byref(_centroid(centroid)),
+    C.check(C.load().adakv_plan(ctypes.byref(g), ctypes.byref(_q(q)),
+                                ctypes.byref(_centroid(centroid, D, estimator)),
                                 _ptr(_seq_lens(seq_lens, dev)), ctypes.byref(cb), ctypes.byref(sel),
                                 _ptr(ws), ws.numel(), _stream(dev)), "plan")
     return table, sel_lens
@@ -271,9 +307,11 @@ def sparse_decode(q, k, v, table, sel_lens, block_size: int, sm_scale=None, seq_
 
 
 def decode_fused(q, k, v, centroid, block_size: int, budget: BudgetParams, seq_lens=None,
-                 append_new: int = 0, sm_scale=None, out=None, return_selection=False):
-    """One decode step: optional centroid append, plan, sparse decode
-    (adakv/attention.py:250-268)."""
+                 append_new: int = 0, sm_scale=None, out=None, return_selection=False,
+                 estimator: str | None = None):
+    """One decode step: optional summary append, plan, sparse decode
+    (adakv/attention.py:250-268).  ``centroid`` holds centroids or minmax
+    bounds (the estimator, by its row length)."""
     dev = _on_device(q, k, v, centroid, seq_lens, out)
     B, Hq, D = q.shape
     _, Hkv, S, _ = k.shape
@@ -295,7 +333,7 @@ def decode_fused(q, k, v, centroid, block_size: int, budget: BudgetParams, seq_l
     nbytes = C.load().adakv_workspace_bytes(ctypes.byref(g), T)
     ws = workspace(dev, nbytes)
     C.check(C.load().adakv_decode_fused(ctypes.byref(g), ctypes.byref(_q(q)), ctypes.byref(_kv(k, v)),
-                                        ctypes.byref(_centroid(centroid)),
+                                        ctypes.byref(_centroid(centroid, D, estimator)),
                                         _ptr(_seq_lens(seq_lens, dev)), ctypes.byref(cb), sel_ref,
                                         int(append_new), ctypes.c_float(sm_scale),
                                         ctypes.byref(_out(out)), _ptr(ws), ws.numel(), _stream(dev)),

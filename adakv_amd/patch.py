@@ -7,10 +7,11 @@
     disable_adakv()
 
 Prefill (q_len > 1) and disabled calls go to HF's SDPA, as in the reference
-(patch.py:96-100).  Single-token decode steps run the HIP pipeline.  Unlike the
-reference, which rebuilds every centroid from the full K on every step
-(patch.py:110), each layer keeps its centroids in HBM across steps and only
-the trailing block is refreshed; batches with B > 1 are decoded sparsely when
+(patch.py:96-100).  Single-token decode steps run the HIP pipeline with the
+configured estimator ("centroid", or "minmax" for the Quest bound).  Unlike
+the reference, which rebuilds every block summary from the full K on every
+step (patch.py:110), each layer keeps its summaries in HBM across steps and
+only the trailing block is refreshed; batches with B > 1 are decoded sparsely when
 HF passes no attention mask (equal-length, unpadded batches), and fall back to
 SDPA otherwise.
 """
@@ -37,15 +38,17 @@ _SDPA = ALL_ATTENTION_FUNCTIONS["sdpa"]
 
 
 class _LayerState:
-    """Per-layer centroids [B, Hkv, capacity_blocks, D] kept across decode steps."""
+    """Per-layer block summaries kept across decode steps: centroids
+    [B, Hkv, capacity_blocks, D] or minmax bounds [B, Hkv, capacity_blocks, 2*D]."""
 
-    def __init__(self, key, block_size, centroid_dtype):
+    def __init__(self, key, block_size, centroid_dtype, estimator):
         B, Hkv, S, D = key.shape
         nb = ops.n_blocks(S, block_size)
-        cdt = centroid_dtype or (torch.float32 if key.dtype == torch.float32 else key.dtype)
-        self.sig = (B, Hkv, D, key.dtype, key.device, block_size, cdt)
-        self.centroid = torch.zeros(B, Hkv, nb + max(64, nb // 8), D, dtype=cdt, device=key.device)
-        ops.centroid_build(key, block_size, centroid=self.centroid)
+        cdt = _summary_dtype(key, centroid_dtype, estimator)
+        self.sig = (B, Hkv, D, key.dtype, key.device, block_size, cdt, estimator)
+        row = 2 * D if estimator == "minmax" else D
+        self.centroid = torch.zeros(B, Hkv, nb + max(64, nb // 8), row, dtype=cdt, device=key.device)
+        ops.centroid_build(key, block_size, centroid=self.centroid, estimator=estimator)
         self.seq_len = S
 
     def grow(self, nb):
@@ -62,10 +65,17 @@ class _LayerState:
 _STATE: dict[int, _LayerState] = {}
 
 
+def _summary_dtype(key, centroid_dtype, estimator):
+    cdt = centroid_dtype or (torch.float32 if key.dtype == torch.float32 else key.dtype)
+    if estimator == "minmax" and cdt not in (key.dtype, torch.float32):
+        cdt = torch.float32          # minmax bounds stay exact: key dtype or fp32
+    return cdt
+
+
 def _signature(key, cfg):
     B, Hkv, S, D = key.shape
-    cdt = cfg.get("centroid_dtype") or (torch.float32 if key.dtype == torch.float32 else key.dtype)
-    return (B, Hkv, D, key.dtype, key.device, cfg["block_size"], cdt)
+    cdt = _summary_dtype(key, cfg.get("centroid_dtype"), cfg["estimator"])
+    return (B, Hkv, D, key.dtype, key.device, cfg["block_size"], cdt, cfg["estimator"])
 
 
 def _budget(cfg):
@@ -91,15 +101,13 @@ def adakv_attention_forward(module, query, key, value, attention_mask, scaling, 
     if cfg.get("selection", "adakv") != "adakv":
         raise NotImplementedError(
             f"selection={cfg['selection']!r} (eviction baselines) is not part of the HIP path")
-    if cfg["estimator"] != "centroid":
-        if cfg["estimator"] == "minmax":
-            raise NotImplementedError("the minmax (Quest) estimator has no HIP kernel yet")
+    if cfg["estimator"] not in ("centroid", "minmax"):
         raise ValueError(f"unknown estimator: {cfg['estimator']!r}")
     bs = int(cfg["block_size"])
     S = key.shape[2]
     st = _STATE.get(id(module))
     if st is None or st.sig != _signature(key, cfg) or S < st.seq_len:
-        st = _LayerState(key, bs, cfg.get("centroid_dtype"))
+        st = _LayerState(key, bs, cfg.get("centroid_dtype"), cfg["estimator"])
         _STATE[id(module)] = st
         append_new = 0
     else:
@@ -109,7 +117,7 @@ def adakv_attention_forward(module, query, key, value, attention_mask, scaling, 
     out = torch.empty(B, 1, Hq, D, dtype=query.dtype, device=query.device)
     res = ops.decode_fused(query[:, :, 0, :], key, value, st.centroid, bs, _budget(cfg),
                            append_new=append_new, sm_scale=scaling, out=out[:, 0],
-                           return_selection=instrumentation_active())
+                           return_selection=instrumentation_active(), estimator=cfg["estimator"])
     if instrumentation_active():
         _, table, lens = res
         record_selection(table, lens, ops.n_blocks(S, bs))

@@ -12,7 +12,9 @@
  * Layouts (element strides; head_dim is always the contiguous axis):
  *   query    [batch, n_q_heads, head_dim]
  *   K, V     [batch, n_kv_heads, max_seq_len, head_dim]   (one stride set for both)
- *   centroid [batch, n_kv_heads, max_blocks, head_dim]    (contiguous)
+ *   centroid [batch, n_kv_heads, max_blocks, head_dim]    (contiguous; kind CENTROID)
+ *   minmax   [batch, n_kv_heads, max_blocks, 2*head_dim]  (contiguous; kind MINMAX:
+ *            per block, the per-dimension max of its keys, then their min)
  *   table    [batch, n_q_heads, table_width] int32, sel_lens [batch, n_q_heads] int32
  *   output   [batch, n_q_heads, head_dim]
  * seq_lens is a device int32 array [batch] of true token counts, or NULL when
@@ -22,9 +24,12 @@
  * Reference interfaces replaced (liukefan821/adakv):
  *   adakv_centroid_build   <- AdaKVCache.append_prefill          adakv/attention.py:119-139
  *                             build_block_summaries("centroid")  adakv/estimator.py:27-48
+ *                             build_block_summaries("minmax")    adakv/estimator.py:50-57
+ *                             (kind MINMAX; AdaKVCache.kmin/kmax, adakv/attention.py:131-138)
  *   adakv_centroid_append  <- update_cache_decode                adakv/runtime.py:43-60
  *                             (and the TODO AdaKVCache.append_decode, adakv/attention.py:141-146)
  *   adakv_block_scores     <- block_scores("centroid")           adakv/estimator.py:62-74
+ *                             block_scores("minmax")             adakv/estimator.py:76-79
  *   adakv_plan             <- plan_selection                     adakv/attention.py:149-247
  *                             (estimator.py:62-74, budget.py:45-86, selector.py:18-60)
  *   adakv_sparse_decode    <- block_sparse_decode                adakv/kernels/block_sparse_decode.py:103-135
@@ -42,7 +47,7 @@
 extern "C" {
 #endif
 
-#define ADAKV_ABI_VERSION 1
+#define ADAKV_ABI_VERSION 2
 
 /* Status codes.  Argument errors are detected on the host before any launch. */
 enum {
@@ -57,6 +62,9 @@ enum {
 };
 
 enum { ADAKV_F32 = 0, ADAKV_F16 = 1, ADAKV_BF16 = 2 };
+
+/* Block summary kinds (the reference's estimator argument, adakv/attention.py:185-198). */
+enum { ADAKV_SUMMARY_CENTROID = 0, ADAKV_SUMMARY_MINMAX = 1 };
 
 /* Budget policies (adakv/budget.py:45-86).  "adaptive_nucleus" is not built. */
 enum { ADAKV_POLICY_FIXED = 0, ADAKV_POLICY_ADAPTIVE = 1 };
@@ -90,9 +98,13 @@ typedef struct {        /* K and V caches [batch, n_kv_heads, max_seq_len, head_
   int64_t stride_b, stride_h, stride_s;
 } adakv_kv_t;
 
-typedef struct {        /* centroids [batch, n_kv_heads, max_blocks, head_dim], contiguous */
+typedef struct {        /* block summaries, contiguous: [batch, n_kv_heads, max_blocks, row]   */
   void* data;
   int32_t dtype;        /* ADAKV_F32 (exact selection parity) or ADAKV_BF16 / ADAKV_F16 */
+  int32_t kind;         /* ADAKV_SUMMARY_CENTROID: row = head_dim (the block's mean key);
+                         * ADAKV_SUMMARY_MINMAX: row = 2*head_dim, [max | min] of the
+                         * block's keys per dimension; head_dim <= 128, dtype the key
+                         * dtype or ADAKV_F32 (both exact)                              */
 } adakv_centroid_t;
 
 typedef struct {        /* plan_selection keyword arguments (adakv/attention.py:149-162) */
@@ -121,25 +133,28 @@ int32_t adakv_table_width(const adakv_geometry_t* g, const adakv_budget_t* p);
 /* Workspace bytes for plan / decode / fused / dense calls on this geometry. */
 size_t adakv_workspace_bytes(const adakv_geometry_t* g, int32_t table_width);
 
-/* Mean key of every block over its real tokens (sequential fp32 sum / count),
- * stored in the centroid dtype.  adakv/estimator.py:27-48, adakv/attention.py:119-139. */
+/* Summary of every block over its real tokens: the mean key (sequential fp32
+ * sum / count, stored in the centroid dtype; adakv/estimator.py:27-48,
+ * adakv/attention.py:119-139) or, for kind MINMAX, the per-dimension max and
+ * min of its keys (adakv/estimator.py:50-57, adakv/attention.py:131-138). */
 int adakv_centroid_build(const adakv_geometry_t* g, const adakv_kv_t* kv, const int32_t* seq_lens,
                          const adakv_centroid_t* centroid, void* stream);
 
 /* After n_new tokens were written at positions [len-n_new, len) of every
- * sequence, recompute the centroids of the blocks holding them (O(block_size*D)
+ * sequence, recompute the summaries of the blocks holding them (O(block_size*D)
  * per KV head; identical bits to a full rebuild).  adakv/runtime.py:43-60. */
 int adakv_centroid_append(const adakv_geometry_t* g, const adakv_kv_t* kv, const int32_t* seq_lens,
                           int32_t n_new, const adakv_centroid_t* centroid, void* stream);
 
-/* Block scores q . centroid for every (sequence, q-head, block), fp32, no
- * 1/sqrt(D) (adakv/estimator.py:62-74).  scores [batch, n_q_heads, pitch] with
+/* Block scores for every (sequence, q-head, block), fp32, no 1/sqrt(D):
+ * q . centroid (adakv/estimator.py:62-74) or, for kind MINMAX, the Quest bound
+ * max(q,0) . kmax + min(q,0) . kmin (adakv/estimator.py:76-79).  scores [batch, n_q_heads, pitch] with
  * pitch >= max_blocks; entries past a sequence's last block are left untouched. */
 int adakv_block_scores(const adakv_geometry_t* g, const adakv_query_t* q,
                        const adakv_centroid_t* centroid, const int32_t* seq_lens, float* scores,
                        int32_t pitch, void* stream);
 
-/* Score every block by q . centroid, split the mean-pinned budget across the
+/* Score every block (as adakv_block_scores), split the mean-pinned budget across the
  * heads of each sequence, select sink + local + top-scoring blocks.
  * Rows list forced blocks (ascending) then content blocks by descending score
  * (ties: lower block id first); entries past sel_lens are never read (further
@@ -157,7 +172,7 @@ int adakv_sparse_decode(const adakv_geometry_t* g, const adakv_query_t* q, const
                         const adakv_output_t* out, void* workspace, size_t workspace_bytes,
                         void* stream);
 
-/* One decode step: optional centroid append of the newest append_new tokens,
+/* One decode step: optional summary append of the newest append_new tokens,
  * plan, sparse decode.  sel may be NULL (selection kept in the workspace) or
  * name caller buffers that receive the selection.  adakv/attention.py:250-268. */
 int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,

@@ -139,6 +139,40 @@ def test_centroid_dtype_pairs(lib):
                                      None) == C.ADAKV_ERR_VALUE          # n_new must be >= 1
 
 
+def test_minmax_summary_validation(lib):
+    """Summary kinds: an unknown kind is a bad value, minmax rows need head_dim
+    <= 128 and an exact element type (the key type or fp32)."""
+    kv32 = C.KV(0x1000, 0, C.ADAKV_F32, 0, 131072 * 128, 128)
+    kv16 = C.KV(0x1000, 0, C.ADAKV_BF16, 0, 131072 * 128, 128)
+    g = _g()
+    build = lambda geo, kv, c: lib.adakv_centroid_build(ctypes.byref(geo), ctypes.byref(kv), None,
+                                                        ctypes.byref(c), None)
+    assert build(g, kv16, C.Centroid(0x4000, C.ADAKV_BF16, 7)) == C.ADAKV_ERR_VALUE
+    assert build(g, kv32, C.Centroid(0x4000, C.ADAKV_BF16, C.SUMMARY_MINMAX)) == C.ADAKV_ERR_DTYPE
+    assert build(g, kv16, C.Centroid(0x4000, C.ADAKV_F16, C.SUMMARY_MINMAX)) == C.ADAKV_ERR_DTYPE
+    g256 = _g(D=256, Hq=8, Hkv=8)
+    assert build(g256, kv16, C.Centroid(0x4000, C.ADAKV_BF16, C.SUMMARY_MINMAX)) == \
+        C.ADAKV_ERR_UNSUPPORTED
+    q = C.Query(0x1000, C.ADAKV_BF16, 4096, 128)
+    assert lib.adakv_block_scores(ctypes.byref(g256), ctypes.byref(q),
+                                  ctypes.byref(C.Centroid(0x4000, C.ADAKV_F32, C.SUMMARY_MINMAX)),
+                                  None, ctypes.c_void_p(0x8000), 8192, None) == C.ADAKV_ERR_UNSUPPORTED
+
+
+def test_summary_kind_from_the_row_length():
+    """ops infers the estimator from the summary's last dimension."""
+    import torch
+    assert ops.summary_kind(torch.zeros(1, 2, 4, 64), 64) == "centroid"
+    assert ops.summary_kind(torch.zeros(1, 2, 4, 128), 64) == "minmax"
+    assert ops.summary_kind(torch.zeros(1, 2, 4, 128), 64, "minmax") == "minmax"
+    with pytest.raises(ValueError):
+        ops.summary_kind(torch.zeros(1, 2, 4, 64), 64, "minmax")
+    with pytest.raises(ValueError):
+        ops.summary_kind(torch.zeros(1, 2, 4, 96), 64)
+    with pytest.raises(ValueError):
+        ops.summary_kind(torch.zeros(1, 2, 4, 64), 64, "bogus")
+
+
 def test_workspace_bytes_grows_with_the_problem(lib):
     small, big = _g(max_seq_len=4096, max_blocks=256), _g()
     assert 0 < lib.adakv_workspace_bytes(ctypes.byref(small), 64) < \
@@ -164,6 +198,8 @@ def test_python_errors_mirror_the_reference(lib):
         plan_selection(torch.zeros(4, 32), cache, 8, budget_policy="nope")
     with pytest.raises(ValueError):
         plan_selection(torch.zeros(4, 32), cache, 8, estimator="minmax")
+    with pytest.raises(RuntimeError):
+        AdaKVCache(16, estimator="minmax").append_prefill(torch.zeros(2, 64, 32), torch.zeros(2, 64, 32))
     with pytest.raises(NotImplementedError):
         ops.BudgetParams(budget_policy="adaptive_nucleus").to_c()
     with pytest.raises(RuntimeError):

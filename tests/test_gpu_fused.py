@@ -50,13 +50,23 @@ def _rounded(x: np.ndarray, dt) -> np.ndarray:
     return torch.from_numpy(x).to(dt).float().numpy()
 
 
+def summary_of(c: np.ndarray, Hq: int, est: str) -> dict:
+    """The oracle's summary dict from GPU summaries [Hkv, nb, D] (centroid) or
+    [Hkv, nb, 2D] (minmax rows [max | min]), expanded to the q-heads."""
+    c = O.expand_gqa(c.astype(np.float32), Hq)
+    if est == "minmax":
+        D = c.shape[-1] // 2
+        return {"kind": "minmax", "kmax": np.ascontiguousarray(c[..., :D]),
+                "kmin": np.ascontiguousarray(c[..., D:])}
+    return {"kind": "centroid", "centroid": c}
+
+
 def _check_sequence(q, K, V, c, table, lens, out, p, bs, tag):
     """One sequence: q [Hq, D], K/V [Hkv, S, D] (the rounded values), c the
-    GPU centroids [Hkv, nb, D]; table [Hq, T], lens [Hq], out [Hq, D]."""
+    GPU summaries [Hkv, nb, D or 2D]; table [Hq, T], lens [Hq], out [Hq, D]."""
     Hq, Hkv = q.shape[0], K.shape[0]
     nb = c.shape[1]
-    cent = O.expand_gqa(c.astype(np.float32), Hq)
-    scores = O.block_scores(q, {"kind": "centroid", "centroid": cent})
+    scores = O.block_scores(q, summary_of(c, Hq, p.get("est", "centroid")))
     lo, _, target, _ = O.budget_bounds(nb, p["avg"], p["kmin"], p["kmax"], p["sink"], p["local"], p["cmin"])
     floor = min(p["sink"], nb) + min(p["local"], nb) + p["cmin"]
     k = O.allocate_budget(scores, p["avg"], min(p["kmin"], nb), min(p["kmax"], nb),
@@ -78,21 +88,22 @@ def _run(q, K, V, p, bs, dt, seq_lens=None, append_new=0, corrupt_tail=0):
     kd = torch.from_numpy(K).to(dt).to(DEV)
     vd = torch.from_numpy(V).to(dt).to(DEV)
     sl = None if seq_lens is None else torch.tensor(seq_lens, dtype=torch.int32, device=DEV)
+    est = p.get("est", "centroid")
     if corrupt_tail:
-        # centroids built while the newest tokens still held other keys: the
+        # summaries built while the newest tokens still held other keys: the
         # step's append must recompute those blocks from the real keys
         kstale = kd.clone()
         kstale[:, :, K.shape[2] - corrupt_tail:] = 7.0
-        c = ops.centroid_build(kstale, bs, seq_lens=sl, centroid_dtype=dt)
+        c = ops.centroid_build(kstale, bs, seq_lens=sl, centroid_dtype=dt, estimator=est)
     else:
-        c = ops.centroid_build(kd, bs, seq_lens=sl, centroid_dtype=dt)
+        c = ops.centroid_build(kd, bs, seq_lens=sl, centroid_dtype=dt, estimator=est)
     out, table, lens = ops.decode_fused(qd, kd, vd, c, bs, _budget(ops, p), seq_lens=sl,
-                                        append_new=append_new, return_selection=True)
+                                        append_new=append_new, return_selection=True, estimator=est)
     torch.cuda.synchronize()
     if corrupt_tail:
-        fresh = ops.centroid_build(kd, bs, seq_lens=sl, centroid_dtype=dt)
+        fresh = ops.centroid_build(kd, bs, seq_lens=sl, centroid_dtype=dt, estimator=est)
         torch.cuda.synchronize()
-        assert torch.equal(c, fresh), "appended blocks' centroids differ from a rebuild"
+        assert torch.equal(c, fresh), "appended blocks' summaries differ from a rebuild"
     qr, Kr, Vr = _rounded(q, dt), _rounded(K, dt), _rounded(V, dt)
     c_np, table, lens, out = c.float().cpu().numpy(), table.cpu().numpy(), lens.cpu().numpy(), \
         out.float().cpu().numpy()

@@ -109,6 +109,21 @@ def _alloc_floor(scores, avg_budget, k_min, k_max, temperature=1.0, policy="adap
     return np.clip(np.floor(lo + O.budget_extra(w, lo, target)), lo, hi).astype(np.int64)
 
 
+def _minmax_bounds_swapped(q, summ):
+    if summ["kind"] != "minmax":
+        return O.block_scores(q, summ)
+    return O.block_scores(q, dict(summ, kmax=summ["kmin"], kmin=summ["kmax"]))
+
+
+def _minmax_from_padded_blocks(keys, bs, kind="centroid"):
+    if kind != "minmax":
+        return O.build_block_summaries(keys, bs, kind)
+    H, S, D = keys.shape
+    nb = -(-S // bs)
+    kp = np.concatenate([keys, np.zeros((H, nb * bs - S, D), np.float32)], 1).reshape(H, nb, bs, D)
+    return {"kind": "minmax", "n_blocks": nb, "n_real": S, "kmin": kp.min(2), "kmax": kp.max(2)}
+
+
 def _select_no_local(scores, k, n_sink_blocks=1, n_local_blocks=4, c_min=1):
     return O.select_blocks(scores, k, n_sink_blocks, 0, c_min + n_local_blocks)
 
@@ -125,13 +140,26 @@ MUTANTS = {
     "local_window_not_forced": dict(select_blocks=_select_no_local),
     "selection_sign_flipped": dict(select_blocks=_select_ascending),
     "attention_scale_missing": dict(attn_scale=lambda d: 1.0),
+    "minmax_bounds_swapped": dict(block_scores=_minmax_bounds_swapped),
 }
+
 
 
 @pytest.mark.parametrize("mutant", sorted(MUTANTS))
 def test_planted_mistake_is_caught(mutant):
     m = _mutant(**MUTANTS[mutant])
     caught = []
-    for name in ("partial_tail", "cfg1_seed0", "temp_sink_local", "peaked_mixed"):
+    for name in ("partial_tail", "cfg1_seed0", "temp_sink_local", "peaked_mixed", "minmax_fixed"):
         caught += golden_check.check_case(m, name)
     assert caught, f"mutant {mutant} passed the golden checks"
+
+
+def test_minmax_padding_mistake_is_caught_by_a_closed_form():
+    """A partial last block padded with zeros before min / max: the bounds of
+    one-token blocks must equal the token itself."""
+    rng = np.random.default_rng(3)
+    K = (rng.standard_normal((2, 33, 8)).astype(np.float32) + np.float32(5.0))   # all positive
+    for build, ok in ((O.build_block_summaries, True), (_minmax_from_padded_blocks, False)):
+        s = build(K, 16, "minmax")
+        exact = np.array_equal(s["kmin"][:, 2], K[:, 32]) and np.array_equal(s["kmax"][:, 2], K[:, 32])
+        assert exact == ok

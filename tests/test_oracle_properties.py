@@ -101,6 +101,36 @@ def test_scores_match_fp64_brute_force():
     assert np.abs(s - ref).max() <= 1e-5 * np.abs(ref).max()
 
 
+def test_minmax_bound_dominates_every_key_of_its_block():
+    """Quest's bound (estimator.py:76-79) is >= q . k for every real key of the
+    block, with equality for one-token blocks and for blocks whose keys are
+    all equal; the bounds are the per-dimension extremes over real tokens."""
+    rng = np.random.default_rng(11)
+    H, S, D, bs = 3, 16 * 9 + 1, 32, 16          # last block: one token
+    q = rng.standard_normal((H, D)).astype(np.float32)
+    K = rng.standard_normal((H, S, D)).astype(np.float32)
+    K[:, 16:32] = K[:, 16:17]                     # block 1: every key equal
+    summ = O.build_block_summaries(K, bs, "minmax")
+    nb = summ["n_blocks"]
+    assert nb == 10
+    for b in range(nb):
+        blk = K[:, b * bs:min(S, (b + 1) * bs)]
+        assert np.array_equal(summ["kmax"][:, b], blk.max(axis=1))
+        assert np.array_equal(summ["kmin"][:, b], blk.min(axis=1))
+    s = O.block_scores(q, summ).astype(np.float64)
+    q64, K64 = q.astype(np.float64), K.astype(np.float64)
+    for b in range(nb):
+        dots = np.einsum("hd,hsd->hs", q64, K64[:, b * bs:min(S, (b + 1) * bs)])
+        assert np.all(s[:, b] >= dots.max(axis=1) - 1e-4)
+        if b in (1, nb - 1):
+            assert np.allclose(s[:, b], dots[:, 0], rtol=0, atol=1e-4)
+    # closed form on one dimension: q > 0 picks the max, q < 0 the min
+    one = O.block_scores(np.array([[2.0, -3.0]], np.float32),
+                         {"kind": "minmax", "kmax": np.array([[[1.0, 4.0]]], np.float32),
+                          "kmin": np.array([[[-1.0, -2.0]]], np.float32)})
+    assert one[0, 0] == np.float32(2.0 * 1.0 + -3.0 * -2.0)
+
+
 def test_entropy_weight_closed_forms():
     flat = np.zeros((1, 256), np.float32)
     w = O.budget_weights(flat)
