@@ -25,9 +25,9 @@ ADAKV_ERR_LAUNCH = 6
 ADAKV_ERR_VALUE = 7
 
 ADAKV_F32, ADAKV_F16, ADAKV_BF16 = 0, 1, 2
-POLICY_FIXED, POLICY_ADAPTIVE = 0, 1
+POLICY_FIXED, POLICY_ADAPTIVE, POLICY_NUCLEUS = 0, 1, 2
 SUMMARY_CENTROID, SUMMARY_MINMAX = 0, 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class Geometry(ctypes.Structure):
@@ -58,7 +58,7 @@ class Centroid(ctypes.Structure):
 class Budget(ctypes.Structure):
     _fields_ = [("avg_budget", ctypes.c_double), ("k_min", c_int32), ("k_max", c_int32),
                 ("n_sink_blocks", c_int32), ("n_local_blocks", c_int32), ("c_min", c_int32),
-                ("temperature", ctypes.c_double), ("policy", c_int32)]
+                ("temperature", ctypes.c_double), ("policy", c_int32), ("nucleus_p", ctypes.c_double)]
 
 
 class Selection(ctypes.Structure):

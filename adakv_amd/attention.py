@@ -210,10 +210,11 @@ class AdaKVCache:
 
 
 def _budget(avg_budget, k_min, k_max, n_sink_blocks, n_local_blocks, temperature, budget_policy,
-            c_min):
+            c_min, nucleus_p=0.9):
     return ops.BudgetParams(avg_budget=avg_budget, k_min=k_min, k_max=k_max,
                             n_sink_blocks=n_sink_blocks, n_local_blocks=n_local_blocks,
-                            c_min=c_min, temperature=temperature, budget_policy=budget_policy)
+                            c_min=c_min, temperature=temperature, budget_policy=budget_policy,
+                            nucleus_p=nucleus_p)
 
 
 def _validate(cache, estimator, budget_policy):
@@ -239,7 +240,7 @@ def plan_selection(q, cache: AdaKVCache, avg_budget, k_min: int = 2, k_max: int 
     """
     summ = _validate(cache, estimator, budget_policy)
     budget = _budget(avg_budget, k_min, k_max, n_sink_blocks, n_local_blocks, temperature,
-                     budget_policy, c_min)
+                     budget_policy, c_min, nucleus_p)
     table, lens = ops.plan(q.unsqueeze(0), summ, cache.block_size, budget,
                            seq_len=cache.seq_len, estimator=estimator)
     block_table, sel_lens = table[0], lens[0]
@@ -250,12 +251,13 @@ def plan_selection(q, cache: AdaKVCache, avg_budget, k_min: int = 2, k_max: int 
 def adakv_decode_attention(q, cache: AdaKVCache, avg_budget, k_min: int = 2, k_max: int = 64,
                            n_sink_blocks: int = 1, n_local_blocks: int = 4,
                            temperature: float = 1.0, estimator: str = "centroid",
-                           budget_policy: str = "adaptive", c_min: int = 1):
-    """One AdaKV decode step: plan + sparse decode in one C call (three
-    kernels, no host sync).  q: [Hq, D] -> [Hq, D] (adakv/attention.py:250-268)."""
+                           budget_policy: str = "adaptive", c_min: int = 1, nucleus_p: float = 0.9):
+    """One AdaKV decode step: plan + sparse decode in one C call (two or three
+    kernels, no host sync).  q: [Hq, D] -> [Hq, D] (adakv/attention.py:250-268;
+    the estimator / policy keywords are plan_selection's)."""
     summ = _validate(cache, estimator, budget_policy)
     budget = _budget(avg_budget, k_min, k_max, n_sink_blocks, n_local_blocks, temperature,
-                     budget_policy, c_min)
+                     budget_policy, c_min, nucleus_p)
     D = q.shape[-1]
     res = ops.decode_fused(q.unsqueeze(0), cache.k.unsqueeze(0), cache.v.unsqueeze(0), summ,
                            cache.block_size, budget, sm_scale=1.0 / math.sqrt(D),

@@ -96,8 +96,10 @@ int check_centroid(const adakv_geometry_t* g, const adakv_centroid_t* c) {
 
 int check_budget(const adakv_budget_t* p) {
   if (!p) return ADAKV_ERR_NULL;
-  if (p->policy != ADAKV_POLICY_FIXED && p->policy != ADAKV_POLICY_ADAPTIVE) return ADAKV_ERR_VALUE;
+  if (p->policy != ADAKV_POLICY_FIXED && p->policy != ADAKV_POLICY_ADAPTIVE && p->policy != ADAKV_POLICY_NUCLEUS)
+    return ADAKV_ERR_VALUE;
   if (!isfinite(p->avg_budget) || !isfinite(p->temperature)) return ADAKV_ERR_VALUE;
+  if (p->policy == ADAKV_POLICY_NUCLEUS && !isfinite(p->nucleus_p)) return ADAKV_ERR_VALUE;
   if (p->k_min < 0 || p->k_max < 0 || p->n_sink_blocks < 0 || p->n_local_blocks < 0 || p->c_min < 0)
     return ADAKV_ERR_VALUE;
   return ADAKV_OK;
@@ -147,6 +149,7 @@ BudgetCfg budget_cfg(const adakv_budget_t* p) {
   c.sink = p->n_sink_blocks; c.local = p->n_local_blocks; c.c_min = p->c_min;
   c.policy = p->policy;
   c.temperature = p->temperature;
+  c.nucleus_p = (float)p->nucleus_p;
   return c;
 }
 
@@ -225,6 +228,8 @@ int run_plan(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_cent
   SelectArgs se;
   int st;
   if ((st = run_scores(g, q, c, kv_append, n_new, lens, p, table, T, ws, s, &se))) return st;
+  if (p->policy == ADAKV_POLICY_NUCLEUS && launch_nucleus(se, g->max_blocks, s) != hipSuccess)
+    return ADAKV_ERR_LAUNCH;
   if (launch_select(se, g->max_blocks, s) != hipSuccess) return ADAKV_ERR_LAUNCH;
   if (!sel_lens) return ADAKV_OK;
   BudgetArgs ba{};
@@ -457,13 +462,15 @@ int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const 
   if (append_new > 0 && !centroid_pair_ok(kv->dtype, c)) return ADAKV_ERR_DTYPE;
   // bf16 / fp16 K/V (and q of the same type, 16-byte aligned rows) on a shape the fused kernel
   // serves: scores, then one kernel for the budget, the selection and the
-  // decode of every head
+  // decode of every head (the nucleus policy adds its weight kernel in between)
   if (kv->dtype != ADAKV_F32 && q->dtype == kv->dtype && aligned16(q->data) && q->stride_b % 8 == 0 &&
       q->stride_h % 8 == 0 &&
       select_decode_supported(g->head_dim, g->max_blocks, T, g->n_q_heads, L.sp, L.parts_pitch) &&
       select_decode_lds(g->head_dim, g->n_q_heads, g->max_blocks) <= max_lds_per_block()) {
     FusedArgs fa{};
     if ((st = run_scores(g, q, c, kv, append_new, seq_lens, p, table, Tl, w, s, &fa.s))) return st;
+    if (p->policy == ADAKV_POLICY_NUCLEUS && launch_nucleus(fa.s, g->max_blocks, s) != hipSuccess)
+      return ADAKV_ERR_LAUNCH;
     fa.d = decode_args(g, q, kv, seq_lens, sm_scale, out);
     fa.d.sel_lens_out = lens;
     return status_of(launch_select_decode(fa, kv->dtype, g->head_dim, g->max_blocks, s));

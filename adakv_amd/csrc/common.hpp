@@ -287,6 +287,7 @@ struct BudgetCfg {
   double avg;
   int k_min, k_max, sink, local, c_min, policy;
   double temperature;
+  float nucleus_p;             // the nucleus policy's mass target, rounded to fp32 as NumPy compares it
 };
 
 struct Bounds {
@@ -311,7 +312,8 @@ __device__ __forceinline__ Bounds budget_bounds(int nb, const BudgetCfg& p) {
 }
 
 // Selected-block count of one head given its weight w and the sequence's sum of
-// weights (fp64, as NumPy promotes after dividing by np.log(nb)); round half to even.
+// weights (fp64, as NumPy promotes after dividing by np.log(nb) or counting
+// the nucleus); round half to even.  Every policy but fixed shares the formula.
 __device__ __forceinline__ int head_count(const Bounds& r, int policy, double w, double wsum, int Hq) {
   int k;
   if (r.nb <= 1) {

@@ -103,7 +103,7 @@ __device__ Slice build_slice(const DecodeArgs& a, int b, const Grp& gr, int spli
     // counts are known); the counts then decide which of them enter the union.
     const Bounds bb = budget_bounds(nb, a.cfg);
     const bool derive = a.sel_lens == nullptr;
-    const bool adaptive = derive && a.cfg.policy == ADAKV_POLICY_ADAPTIVE && nb > 1;
+    const bool adaptive = derive && a.cfg.policy != ADAKV_POLICY_FIXED && nb > 1;   // weights in wbuf
     const int width = derive ? min(a.T, max(bb.kcap, 0)) : a.T;
     constexpr int EPT = 4;                       // table entries per thread
     int ent[EPT];

@@ -108,7 +108,7 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
   __shared__ int s_list[kSortCap];          // content blocks by rank
   __shared__ float s_m[DW], s_l[DW];
   __shared__ float s_acc[DW][D];            // the decode waves' accumulators for the merge
-  extern __shared__ double s_w[];            // [Hq] entropy weights of the sequence's heads
+  extern __shared__ double s_w[];            // [Hq] budget weights of the sequence's heads
 
   const SelectArgs& a = fa.s;
   const DecodeArgs& d = fa.d;
@@ -122,7 +122,8 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
   const int nf = bb.n_forced;
   const int c_lo = bb.sink, c_hi = nb - bb.local;
   const int local_lo = max(bb.sink, nb - bb.local);
-  const bool adaptive = a.cfg.policy == ADAKV_POLICY_ADAPTIVE && nb > 1;
+  const bool adaptive = a.cfg.policy == ADAKV_POLICY_ADAPTIVE && nb > 1;   // entropy weights from the records
+  const bool nucleus = a.cfg.policy == ADAKV_POLICY_NUCLEUS && nb > 1;     // weights from the nucleus kernel
   int32_t* trow = a.table + ((int64_t)b * Hq + h) * a.T;
   const int64_t oo = (int64_t)b * d.osb + (int64_t)h * d.osh;
   if (nb == 0) {                             // empty sequence: no block, 0/0 as the reference kernel
@@ -253,6 +254,8 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
   };
   // the first pass consumes the records loaded up front, in place
   merge_head(hh0, R0, R1, X0);
+  if (nucleus)                               // written by the nucleus kernel before this launch
+    for (int hh = tid; hh < Hq; hh += NT) s_w[hh] = a.wbuf[(int64_t)b * Hq + hh];
   const int passes = adaptive ? ceil_div(Hq, HPW * NW) : 1;
   for (int p = 1; p < passes; ++p) {         // more than 32 heads
     const int hh = head_of(p);
@@ -281,8 +284,9 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
 
   // ---- 3. the head's count and selection ----
   // every wave evaluates the sum of weights in NumPy's order
-  const double wsum = !adaptive ? 0.0 : Hq <= 128 ? wave_pairwise_sum(s_w, Hq) : numpy_pairwise_sum<6>(s_w, Hq);
-  const int k = min(head_count(bb, a.cfg.policy, adaptive ? s_w[h] : 0.0, wsum, Hq), a.T);
+  const bool weighted = adaptive || nucleus;
+  const double wsum = !weighted ? 0.0 : Hq <= 128 ? wave_pairwise_sum(s_w, Hq) : numpy_pairwise_sum<6>(s_w, Hq);
+  const int k = min(head_count(bb, a.cfg.policy, weighted ? s_w[h] : 0.0, wsum, Hq), a.T);
   if (tid == 0) {
     if (d.sel_lens_out) d.sel_lens_out[(int64_t)b * Hq + h] = k;
     if (adaptive) a.wbuf[(int64_t)b * Hq + h] = s_w[h];

@@ -148,6 +148,8 @@ hipError_t launch_score_minmax(ScoreArgs& a, int cdt, int D, hipStream_t s);
 // Chunks per (sequence, KV head) for any centroid dtype: bound on parts_pitch.
 int score_chunks_max(int max_blocks, int D);
 hipError_t launch_select(const SelectArgs& a, int max_blocks, hipStream_t s);
+// Nucleus weights of every (sequence, q-head) into a.wbuf (ADAKV_POLICY_NUCLEUS).
+hipError_t launch_nucleus(const SelectArgs& a, int max_blocks, hipStream_t s);
 hipError_t launch_budget(const BudgetArgs& a, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs& a, int kvdt, int D, hipStream_t s);
 // Threads per workgroup and static LDS bytes of the decode kernel chosen for

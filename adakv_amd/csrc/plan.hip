@@ -116,6 +116,24 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
   }
 }
 
+// ------------------------------------------------------- nucleus weights ----
+// One workgroup per (sequence, q-head): the nucleus weight of the head's whole
+// score row (adakv/budget.py:38-41) into wbuf, for the consumers of the
+// weights (budget kernel, decode, fused selection).
+template <int NT, int IPT>
+__global__ __launch_bounds__(NT) void nucleus_kernel(SelectArgs a) {
+  __shared__ NucleusLds N;
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
+  const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
+  if (nb <= 1) return;                     // no weight is read: one block takes the k_min rule
+  float v[IPT];
+  load_scores(a.scores + ((int64_t)b * a.Hq + h) * a.sp, nb, v);
+  const float tf = (float)fmax(a.cfg.temperature, 1e-6);
+  const double wn = nucleus_weight<NT, IPT>(N, v, nb, tf, a.cfg.nucleus_p);
+  if (threadIdx.x == 0) a.wbuf[(int64_t)b * a.Hq + h] = wn;
+}
+
 // -------------------------------------------------------------- budgets ----
 __global__ __launch_bounds__(kNT) void budget_kernel(BudgetArgs a) {
   extern __shared__ double s_w[];
@@ -124,7 +142,7 @@ __global__ __launch_bounds__(kNT) void budget_kernel(BudgetArgs a) {
   const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
   const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
   const Bounds bb = budget_bounds(nb, a.cfg);
-  const bool adaptive = a.cfg.policy == ADAKV_POLICY_ADAPTIVE && nb > 1;
+  const bool adaptive = a.cfg.policy != ADAKV_POLICY_FIXED && nb > 1;   // weights in wbuf
   if (adaptive) {
     for (int h = threadIdx.x; h < a.Hq; h += kNT) s_w[h] = a.wbuf[(int64_t)b * a.Hq + h];
     __syncthreads();
@@ -156,6 +174,17 @@ hipError_t launch_select(const SelectArgs& a, int max_blocks, hipStream_t s) {
   else if (max_blocks <= 1024 * 8) hipLaunchKernelGGL((select_kernel<1024, 8>), grid, dim3(1024), 0, s, a);
   else if (max_blocks <= 512 * 32) hipLaunchKernelGGL((select_kernel<512, 32>), grid, dim3(512), 0, s, a);
   else if (max_blocks <= 512 * 64) hipLaunchKernelGGL((select_kernel<512, 64>), grid, dim3(512), 0, s, a);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_nucleus(const SelectArgs& a, int max_blocks, hipStream_t s) {
+  dim3 grid(a.Hq, a.B);
+  if (max_blocks <= 256 * 4) hipLaunchKernelGGL((nucleus_kernel<256, 4>), grid, dim3(256), 0, s, a);
+  else if (max_blocks <= 1024 * 4) hipLaunchKernelGGL((nucleus_kernel<1024, 4>), grid, dim3(1024), 0, s, a);
+  else if (max_blocks <= 1024 * 8) hipLaunchKernelGGL((nucleus_kernel<1024, 8>), grid, dim3(1024), 0, s, a);
+  else if (max_blocks <= 1024 * 16) hipLaunchKernelGGL((nucleus_kernel<1024, 16>), grid, dim3(1024), 0, s, a);
+  else if (max_blocks <= 1024 * 32) hipLaunchKernelGGL((nucleus_kernel<1024, 32>), grid, dim3(1024), 0, s, a);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }

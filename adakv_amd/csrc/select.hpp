@@ -120,6 +120,216 @@ __device__ __forceinline__ double entropy_weight(const SoftPart& p, double lognb
   return (double)(-hs) / lognb + 1e-6;
 }
 
+// ---- the nucleus weight (adakv/budget.py:38-41) -----------------------------
+// w = 1 + #{k : c_k < P}, where c_k is the sum of the k largest block
+// probabilities p = softmax(scores / T) and P the nucleus mass (compared in
+// fp32, as NumPy compares its fp32 cumulative sums with a Python float).
+// Equivalently w = K*, the fewest top blocks whose mass reaches P (nb + 1 when
+// no prefix does).  K* is found without sorting, by a radix search over
+// dist = bits(p_max) - bits(p) (non-negative floats order as their bit
+// patterns, so ascending dist is descending p): each pass histograms the MASS
+// of the remaining candidates per digit of dist and walks the digits upward
+// until the mass before plus the bucket's reaches P.
+//
+// * Pass 1 bins dist >> 19 (1/16-octave steps of p below its maximum), the
+//   last bin collecting everything from 255/16 octaves down; that bin is not
+//   accumulated but derived from the totals, so a peaked head's long tail
+//   costs no atomics.  Passes 2-4 take bits 18..11, 10..3 and 2..0 of dist
+//   within the chosen bin.  Should the crossing fall in the last bin, four
+//   more passes search all 31 bits of dist among the tail's elements.
+// * Masses are exact integers (p * 2^60, truncated), so the passes agree with
+//   each other whatever the order of the atomic additions.
+// * When the passes end, the crossing value p* is known exactly, with
+//   a = #{p > p*} and M their mass; the crossing is the i-th copy of p*,
+//   i = ceil((P - M) / p*), and K* = a + i.
+struct NucleusLds {
+  unsigned long long mass[256];
+  int cnt[256];
+  float fred[16];
+  double dred[16];
+  unsigned long long qred[16];
+  unsigned long long m_above;
+  int n_above, n_at, done;
+  uint32_t prefix;
+};
+
+__device__ __forceinline__ unsigned long long wave_excl_scan_u64(unsigned long long x) {
+  const int lane = threadIdx.x & (kWave - 1);
+  unsigned long long inc = x;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const unsigned long long y = __shfl_up(inc, o);
+    if (lane >= o) inc += y;
+  }
+  return inc - x;
+}
+
+// One pass: candidates are the elements with cand(i), of mass mq(i) and digit
+// digit(i) in [0, 256).  With tail_bin, bin 255 is not accumulated: it holds
+// the rest of m_tot / n_tot.  Returns false (uniformly) when the mass never
+// reaches Pq.  On return N.prefix holds the chosen digit appended to `prefix`.
+template <int NT, int IPT, typename Mass, typename Cand, typename Digit>
+__device__ __forceinline__ bool nucleus_pass(NucleusLds& N, Mass mq, Cand cand, Digit digit,
+                                             unsigned long long Pq, uint32_t prefix, int bits, bool tail_bin,
+                                             unsigned long long m_tot, int n_tot) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  for (int j = tid; j < 256; j += NT) { N.mass[j] = 0ull; N.cnt[j] = 0; }
+  lds_barrier();
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    if (cand(i)) {
+      const int d = digit(i);
+      if (!(tail_bin && d == 255)) {
+        atomicAdd(&N.mass[d], mq(i));
+        atomicAdd(&N.cnt[d], 1);
+      }
+    }
+  }
+  lds_barrier();
+  if (w == 0) {
+    // lane l holds digits 4l .. 4l+3: lane order is digit order
+    unsigned long long bm[4], lm = 0ull;
+    int bc[4], lc = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bm[j] = N.mass[4 * lane + j];
+      bc[j] = N.cnt[4 * lane + j];
+      lm += bm[j];
+      lc += bc[j];
+    }
+    if (tail_bin) {
+      const unsigned long long m_rest = m_tot - wave_sum(lm);
+      const int n_rest = n_tot - wave_sum(lc);
+      if (lane == kWave - 1) { bm[3] = m_rest; bc[3] = n_rest; lm += m_rest; lc += n_rest; }
+    }
+    unsigned long long R = N.m_above + wave_excl_scan_u64(lm);
+    int C = N.n_above + wave_incl_scan(lc) - lc;
+    int hit = -1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (hit < 0) {
+        if (bc[j] > 0 && R + bm[j] >= Pq) {
+          hit = j;
+        } else {
+          R += bm[j];
+          C += bc[j];
+        }
+      }
+    }
+    const uint64_t hits = __ballot(hit >= 0);
+    if (hits != 0 && lane == __builtin_ctzll(hits)) {
+      N.prefix = (prefix << bits) | (uint32_t)(4 * lane + hit);
+      N.m_above = R;
+      N.n_above = C;
+      N.n_at = bc[hit];
+    }
+    if (lane == 0) N.done = hits ? 0 : 1;
+  }
+  lds_barrier();
+  return N.done == 0;
+}
+
+// z: the head's scores (overwritten), thread t owning blocks [t*IPT,
+// (t+1)*IPT); nb > 1.  Every thread receives the weight.  Per element only
+// dist is kept (its mass is recomputed from it), so large IPT stays within
+// the register file.
+template <int NT, int IPT>
+__device__ double nucleus_weight(NucleusLds& N, float (&z)[IPT], int nb, float tf, float nucleus_p) {
+  constexpr int NW = NT / kWave;
+  static_assert(NW <= 16, "per-wave partials");
+  constexpr double kScale = 1152921504606846976.0;   // 2^60
+  constexpr uint32_t kNone = 0xffffffffu;             // dist of blocks >= nb (real dists are < 2^31)
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  const int base = tid * IPT;
+  // z = s / T (in place) and its maximum
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    z[i] = base + i < nb ? (tf == 1.f ? z[i] : __fdiv_rn(z[i], tf)) : -INFINITY;
+    mx = fmaxf(mx, z[i]);
+  }
+  mx = wave_allreduce(mx, OpMax());
+  if (lane == 0) N.fred[w] = mx;
+  lds_barrier();
+  mx = N.fred[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) mx = fmaxf(mx, N.fred[i]);
+  // p = exp(z - max) / sum, the sum taken in fp64 and rounded once to fp32
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    z[i] = z[i] == -INFINITY ? 0.f : expf(z[i] - mx);     // z now holds e = exp(z - max)
+    s += (double)z[i];
+  }
+  s = wave_sum(s);
+  if (lane == 0) N.dred[w] = s;
+  lds_barrier();
+  s = 0.0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) s += N.dred[i];
+  const float s32 = (float)s;
+  const uint32_t kmax = __float_as_uint(__fdiv_rn(1.f, s32));      // p of the largest score: exp(0) / sum
+  uint32_t dist[IPT];
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) dist[i] = base + i < nb ? kmax - __float_as_uint(__fdiv_rn(z[i], s32)) : kNone;
+  auto mq = [&](int i) -> unsigned long long {
+    return (unsigned long long)((double)__uint_as_float(kmax - dist[i]) * kScale);
+  };
+  unsigned long long mloc = 0ull;
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) mloc += dist[i] != kNone ? mq(i) : 0ull;
+  mloc = wave_sum(mloc);
+  if (lane == 0) N.qred[w] = mloc;
+  if (tid == 0) { N.m_above = 0ull; N.n_above = 0; }
+  lds_barrier();
+  unsigned long long m_tot = 0ull;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) m_tot += N.qred[i];
+  const double P = fmin(fmax((double)nucleus_p, 0.0), 2.0);
+  const unsigned long long Pq = (unsigned long long)(P * kScale);
+  auto valid = [&](int i) { return dist[i] != kNone; };
+  // pass 1: 1/16-octave bins below the maximum, the tail in bin 255
+  if (!nucleus_pass<NT, IPT>(N, mq, valid, [&](int i) { return (int)min(dist[i] >> 19, 255u); }, Pq, 0u, 8,
+                             true, m_tot, nb))
+    return (double)(nb + 1);                 // the whole mass stays below P
+  uint32_t pre = N.prefix;
+  uint32_t dstar;
+  if (pre < 255u) {
+    // bits 18..11, 10..3, 2..0 of dist within the bin
+    constexpr int kShift[3] = {11, 3, 0}, kBits[3] = {8, 8, 3};
+#pragma unroll 1
+    for (int ps = 0; ps < 3; ++ps) {
+      const int sh = kShift[ps], nbits = kBits[ps];
+      nucleus_pass<NT, IPT>(N, mq, [&](int i) { return valid(i) && (dist[i] >> (sh + nbits)) == pre; },
+                            [&](int i) { return (int)((dist[i] >> sh) & ((1u << nbits) - 1u)); }, Pq, pre,
+                            nbits, false, 0ull, 0);
+      pre = N.prefix;
+    }
+    dstar = pre;
+  } else {
+    // the crossing lies in the tail: all 31 bits of dist among its elements
+    constexpr uint32_t kTail = 255u << 19;
+    pre = 0u;
+#pragma unroll 1
+    for (int sh = 24; sh >= 0; sh -= 8) {
+      const int nbits = sh == 24 ? 7 : 8;
+      nucleus_pass<NT, IPT>(N, mq,
+                            [&](int i) {
+                              return valid(i) && dist[i] >= kTail && (sh == 24 || (dist[i] >> (sh + 8)) == pre);
+                            },
+                            [&](int i) { return (int)((dist[i] >> sh) & ((1u << nbits) - 1u)); }, Pq, pre,
+                            nbits, false, 0ull, 0);
+      pre = N.prefix;
+    }
+    dstar = pre;
+  }
+  const unsigned long long pstar = (unsigned long long)((double)__uint_as_float(kmax - dstar) * kScale);
+  const unsigned long long need = Pq - N.m_above;     // > 0: the mass before the crossing stays below P
+  int i = pstar > 0 ? (int)((need + pstar - 1) / pstar) : N.n_at;
+  i = min(max(i, 1), N.n_at);
+  return (double)(N.n_above + i);
+}
+
 // ---- the selection ---------------------------------------------------------
 template <int NT>
 struct SelectLds {

@@ -25,8 +25,8 @@ import torch
 from . import _capi as C
 
 _DTYPES = {torch.float32: C.ADAKV_F32, torch.float16: C.ADAKV_F16, torch.bfloat16: C.ADAKV_BF16}
-_POLICIES = {"fixed": C.POLICY_FIXED, "adaptive": C.POLICY_ADAPTIVE}
-_NOT_BUILT_POLICIES = ("adaptive_nucleus",)
+_POLICIES = {"fixed": C.POLICY_FIXED, "adaptive": C.POLICY_ADAPTIVE,
+             "adaptive_nucleus": C.POLICY_NUCLEUS}
 
 
 @dataclass(frozen=True)
@@ -40,17 +40,14 @@ class BudgetParams:
     c_min: int = 1
     temperature: float = 1.0
     budget_policy: str = "adaptive"
+    nucleus_p: float = 0.9
 
     def to_c(self) -> C.Budget:
-        if self.budget_policy in _NOT_BUILT_POLICIES:
-            raise NotImplementedError(
-                f"budget_policy {self.budget_policy!r} has no HIP kernel yet (only 'fixed' and "
-                "'adaptive')")
         if self.budget_policy not in _POLICIES:
             raise ValueError(f"unknown budget_policy: {self.budget_policy!r}")
         return C.Budget(float(self.avg_budget), int(self.k_min), int(self.k_max),
                         int(self.n_sink_blocks), int(self.n_local_blocks), int(self.c_min),
-                        float(self.temperature), _POLICIES[self.budget_policy])
+                        float(self.temperature), _POLICIES[self.budget_policy], float(self.nucleus_p))
 
 
 def _dt(t: torch.Tensor) -> int:

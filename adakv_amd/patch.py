@@ -82,7 +82,8 @@ def _budget(cfg):
     return ops.BudgetParams(avg_budget=cfg["avg_budget"], k_min=cfg["k_min"], k_max=cfg["k_max"],
                             n_sink_blocks=cfg["n_sink_blocks"],
                             n_local_blocks=cfg["n_local_blocks"], c_min=cfg["c_min"],
-                            temperature=cfg["temperature"], budget_policy=cfg["budget_policy"])
+                            temperature=cfg["temperature"], budget_policy=cfg["budget_policy"],
+                            nucleus_p=cfg.get("nucleus_p", 0.9))
 
 
 def adakv_attention_forward(module, query, key, value, attention_mask, scaling, dropout=0.0,

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define ADAKV_ABI_VERSION 2
+#define ADAKV_ABI_VERSION 3
 
 /* Status codes.  Argument errors are detected on the host before any launch. */
 enum {
@@ -66,8 +66,9 @@ enum { ADAKV_F32 = 0, ADAKV_F16 = 1, ADAKV_BF16 = 2 };
 /* Block summary kinds (the reference's estimator argument, adakv/attention.py:185-198). */
 enum { ADAKV_SUMMARY_CENTROID = 0, ADAKV_SUMMARY_MINMAX = 1 };
 
-/* Budget policies (adakv/budget.py:45-86).  "adaptive_nucleus" is not built. */
-enum { ADAKV_POLICY_FIXED = 0, ADAKV_POLICY_ADAPTIVE = 1 };
+/* Budget policies (adakv/budget.py:45-86): fixed top-k, the entropy weight
+ * ("adaptive") and the nucleus weight ("adaptive_nucleus", budget.py:38-41). */
+enum { ADAKV_POLICY_FIXED = 0, ADAKV_POLICY_ADAPTIVE = 1, ADAKV_POLICY_NUCLEUS = 2 };
 
 typedef struct {
   int32_t batch;        /* sequences in the batch (<= 4096, batch*n_kv_heads <= 12288) */
@@ -113,6 +114,7 @@ typedef struct {        /* plan_selection keyword arguments (adakv/attention.py:
   int32_t n_sink_blocks, n_local_blocks, c_min;
   double temperature;
   int32_t policy;
+  double nucleus_p;     /* mass target of ADAKV_POLICY_NUCLEUS (compared in fp32)   */
 } adakv_budget_t;
 
 typedef struct {        /* block_table [batch, n_q_heads, table_width], sel_lens [batch, n_q_heads] */

@@ -116,12 +116,14 @@ def test_plan_validation(lib):
     sel = C.Selection(0x5000, 64, 0x6000)
     narrow = C.Selection(0x5000, 8, 0x6000)
     bad_policy = C.Budget(8.0, 2, 64, 1, 4, 1, 1.0, 5)
+    nan_nucleus = C.Budget(8.0, 2, 64, 1, 4, 1, 1.0, C.POLICY_NUCLEUS, float("nan"))
     neg = C.Budget(8.0, 2, -1, 1, 4, 1, 1.0, 1)
     ok = _b(avg_budget=8)
     f = lib.adakv_plan
     args = lambda b, s: (ctypes.byref(g), ctypes.byref(q), ctypes.byref(c), None, ctypes.byref(b),
                          ctypes.byref(s), ws, 1 << 30, None)
     assert f(*args(bad_policy, sel)) == C.ADAKV_ERR_VALUE
+    assert f(*args(nan_nucleus, sel)) == C.ADAKV_ERR_VALUE
     assert f(*args(neg, sel)) == C.ADAKV_ERR_VALUE
     assert f(*args(ok, narrow)) == C.ADAKV_ERR_SHAPE
     nullsel = C.Selection(0, 64, 0x6000)
@@ -200,8 +202,10 @@ def test_python_errors_mirror_the_reference(lib):
         plan_selection(torch.zeros(4, 32), cache, 8, estimator="minmax")
     with pytest.raises(RuntimeError):
         AdaKVCache(16, estimator="minmax").append_prefill(torch.zeros(2, 64, 32), torch.zeros(2, 64, 32))
-    with pytest.raises(NotImplementedError):
-        ops.BudgetParams(budget_policy="adaptive_nucleus").to_c()
+    assert ops.BudgetParams(budget_policy="adaptive_nucleus", nucleus_p=0.8).to_c().policy == \
+        C.POLICY_NUCLEUS
+    with pytest.raises(ValueError):
+        ops.BudgetParams(budget_policy="nucleus").to_c()
     with pytest.raises(RuntimeError):
         block_sparse_decode(torch.zeros(4, 32), torch.zeros(2, 64, 32), torch.zeros(2, 64, 32),
                             torch.zeros(4, 2, dtype=torch.int32), torch.ones(4, dtype=torch.int32), 16)

@@ -24,7 +24,7 @@ import numpy as np
 import pytest
 
 import cases
-from gpu_util import BF16_ATOL, DEV, REL_L2, compare_selection, need_gpu, rel_l2, say, torch
+from gpu_util import BF16_ATOL, DEV, REL_L2, compare_selection, need_gpu, nucleus_exclusions, rel_l2, say, torch
 from oracle import adakv_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -43,7 +43,8 @@ def _ops():
 def _budget(ops, p):
     return ops.BudgetParams(avg_budget=p["avg"], k_min=p["kmin"], k_max=p["kmax"],
                             n_sink_blocks=p["sink"], n_local_blocks=p["local"], c_min=p["cmin"],
-                            temperature=p["temp"], budget_policy=p["policy"])
+                            temperature=p["temp"], budget_policy=p["policy"],
+                            nucleus_p=p.get("nucleus_p", 0.9))
 
 
 def _rounded(x: np.ndarray, dt) -> np.ndarray:
@@ -69,11 +70,19 @@ def _check_sequence(q, K, V, c, table, lens, out, p, bs, tag):
     scores = O.block_scores(q, summary_of(c, Hq, p.get("est", "centroid")))
     lo, _, target, _ = O.budget_bounds(nb, p["avg"], p["kmin"], p["kmax"], p["sink"], p["local"], p["cmin"])
     floor = min(p["sink"], nb) + min(p["local"], nb) + p["cmin"]
+    P = p.get("nucleus_p", 0.9)
     k = O.allocate_budget(scores, p["avg"], min(p["kmin"], nb), min(p["kmax"], nb),
-                          temperature=p["temp"], policy=p["policy"], floor=floor)
-    w = O.budget_weights(scores, "adaptive", p["temp"])
+                          temperature=p["temp"], policy=p["policy"], nucleus_p=P, floor=floor)
+    w = O.budget_weights(scores, "adaptive_nucleus" if p["policy"] == "adaptive_nucleus" else "adaptive",
+                         p["temp"], P)
+    amb, margin = None, 1e-3
+    if p["policy"] == "adaptive_nucleus" and nb > 1:
+        # nucleus counts on a rounding knife-edge: excluded, and the others'
+        # rounding margin widened by what they would move
+        amb, margin = nucleus_exclusions(scores, lo, target, p["temp"], P)
     excl = compare_selection(scores, table, lens, k_oracle=k, w_oracle=w, lo=lo, target=target,
-                             sink=p["sink"], local=p["local"], cmin=p["cmin"], policy=p["policy"])
+                             sink=p["sink"], local=p["local"], cmin=p["cmin"], policy=p["policy"],
+                             exclude=amb, half_margin=margin)
     ref = O.ref_from_table(q, K, V, table, lens, bs, Hq // Hkv)
     err = float(np.abs(out - ref).max())
     r = rel_l2(out, ref)
