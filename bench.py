@@ -18,7 +18,13 @@ Prints one JSON line: value = microseconds per layer (lower is better), the
 achieved HBM GB/s on the algorithmic bytes of the op, the dense HIP
 flash-decode time at the same context, the roofline of the dominant kernel
 (the centroid scan) timed with HIP events, and the CPU oracle timed on one
-layer of the same workload on this host.
+layer of the same workload on this host.  ``cells`` holds the other methods of
+the reference's decode-latency table (benchmarks/efficiency/
+bench_decode_latency.py:11-19) on the same layers at the same avg_budget:
+quest (minmax bounds + fixed budget), adakv_cf (centroids + fixed budget),
+adakv_nucleus (centroids + the nucleus budget, the cell that table labels
+"adakv"), streaming (sink + most recent blocks, no scoring) and dense, with
+each estimator's summary bytes per layer.
 """
 from __future__ import annotations
 
@@ -48,6 +54,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU-oracle time budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--no-cells", action="store_true", help="skip the quest / adakv_cf / streaming legs")
     ap.add_argument("--seed", type=int, default=0)
     return ap.parse_args()
 
@@ -90,6 +97,40 @@ class Workload:
     def step(self, l):
         self.ops.decode_fused(self.q[l], self.k[l], self.v[l], self.c[l], self.BS, self.budget,
                               append_new=1, out=self.out[l])
+
+    def build_cells(self, avg_budget):
+        """Minmax bounds per layer, the fixed budget, and a streaming table
+        (bench_decode_latency.py:56-63: sink blocks + the most recent window)."""
+        torch, ops = self.torch, self.ops
+        self.m = [ops.centroid_build(k, self.BS, estimator="minmax") for k in self.k]
+        self.fixed = ops.BudgetParams(avg_budget=avg_budget, budget_policy="fixed")
+        self.nucleus = ops.BudgetParams(avg_budget=avg_budget, budget_policy="adaptive_nucleus")
+        bud = int(round(avg_budget))
+        sink = self.budget.n_sink_blocks
+        win = max(bud - sink, 1)
+        idx = torch.cat([torch.arange(0, sink), torch.arange(self.nb - win, self.nb)])[:bud]
+        self.st_table = idx.to(torch.int32).view(1, 1, -1).expand(1, self.Hq, -1).contiguous().cuda()
+        self.st_lens = torch.full((1, self.Hq), idx.numel(), dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+
+    def quest(self, l):
+        self.ops.decode_fused(self.q[l], self.k[l], self.v[l], self.m[l], self.BS, self.fixed,
+                              append_new=1, out=self.out[l])
+
+    def adakv_cf(self, l):
+        self.ops.decode_fused(self.q[l], self.k[l], self.v[l], self.c[l], self.BS, self.fixed,
+                              append_new=1, out=self.out[l])
+
+    def adakv_nucleus(self, l):
+        self.ops.decode_fused(self.q[l], self.k[l], self.v[l], self.c[l], self.BS, self.nucleus,
+                              append_new=1, out=self.out[l])
+
+    def streaming(self, l):
+        self.ops.sparse_decode(self.q[l], self.k[l], self.v[l], self.st_table, self.st_lens, self.BS,
+                               out=self.out[l])
+
+    def minmax_scores(self, l, buf):
+        self.ops.block_scores(self.q[l], self.m[l], self.BS, seq_len=self.S, out=buf)
 
     def dense(self, l):
         self.ops.dense_decode(self.q[l], self.k[l], self.v[l], out=self.out[l])
@@ -259,6 +300,36 @@ def main():
         dense_gbps = (2 * w.Hkv * w.S * w.D * 2) / (dense_us * 1e-6) / 1e9
         log(f"dense flash-decode: {dense_us:.1f} us/layer ({dense_gbps:.0f} GB/s)")
 
+    cells = None
+    if not args.no_cells:
+        w.build_cells(args.avg_budget)
+        cells = {"adakv": {"us_per_layer": round(us_layer, 3), "estimator": "centroid",
+                           "budget_policy": "adaptive",
+                           "summary_bytes_per_layer": int(w.c[0][:, :, : w.nb].numel() * 2)}}
+        for name, fn, est, pol in (("quest", w.quest, "minmax", "fixed"),
+                                   ("adakv_cf", w.adakv_cf, "centroid", "fixed"),
+                                   ("adakv_nucleus", w.adakv_nucleus, "centroid", "adaptive_nucleus"),
+                                   ("streaming", w.streaming, None, "fixed")):
+            g_c = capture(torch, fn, L, stream)
+            ms_c, _ = time_graph(torch, g_c, replays, warm)
+            us_c = ms_c * 1e3 / steps
+            summ = w.m[0] if est == "minmax" else w.c[0] if est == "centroid" else None
+            cells[name] = {"us_per_layer": round(us_c, 3), "estimator": est, "budget_policy": pol,
+                           "summary_bytes_per_layer": 0 if summ is None else int(summ[:, :, : w.nb].numel() * 2)}
+            log(f"{name}: {us_c:.2f} us/layer")
+            del g_c
+        g_ms = capture(torch, lambda l: w.minmax_scores(l, sbuf), L, stream)
+        ms_ms, _ = time_graph(torch, g_ms, replays, warm)
+        us_ms = ms_ms * 1e3 / steps
+        ms_bytes = 2 * nbytes["centroid"] + nbytes["q"] + w.Hq * w.nb * 4
+        cells["quest"]["scan_us"] = round(us_ms, 3)
+        cells["quest"]["scan_GBps"] = round(ms_bytes / (us_ms * 1e-6) / 1e9, 1)
+        log(f"minmax scan: {us_ms:.2f} us/launch, {ms_bytes / (us_ms * 1e-6) / 1e9:.0f} GB/s")
+        del g_ms
+        if dense_us is not None:
+            cells["dense"] = {"us_per_layer": round(dense_us, 2), "estimator": None,
+                              "budget_policy": None, "summary_bytes_per_layer": 0}
+
     cpu = None
     if not args.no_cpu:
         sec, runs = cpu_baseline(torch, w, args.cpu_seconds)
@@ -293,6 +364,7 @@ def main():
                      "launch_us": round(us_sc, 3), "bytes_per_launch": int(sc_bytes),
                      "frac_of_stream_copy": round(sc_gbps / copy_gbps, 4)},
         "cpu_baseline": cpu,
+        "cells": cells,
     }
     print(json.dumps(res), flush=True)
 
