@@ -8,12 +8,21 @@
 
 Prefill (q_len > 1) and disabled calls go to HF's SDPA, as in the reference
 (patch.py:96-100).  Single-token decode steps run the HIP pipeline with the
-configured estimator ("centroid", or "minmax" for the Quest bound).  Unlike
-the reference, which rebuilds every block summary from the full K on every
-step (patch.py:110), each layer keeps its summaries in HBM across steps and
-only the trailing block is refreshed; batches with B > 1 are decoded sparsely when
-HF passes no attention mask (equal-length, unpadded batches), and fall back to
-SDPA otherwise.
+configured estimator ("centroid", or "minmax" for the Quest bound) and budget
+policy.  Differences from the reference hook (patch.py:90-121):
+
+* an SDPA-format mask function is registered for "adakv", so HF builds the
+  masks SDPA would get (the reference registers none, and HF then passes no
+  mask at all: padded batches and static caches were attended unmasked);
+* each layer keeps its block summaries in HBM across steps and refreshes
+  only the blocks that gained tokens (the reference rebuilds them from the
+  whole cache every step, patch.py:110);
+* batches of any size decode sparsely.  With no mask (a dynamic cache and an
+  unpadded batch) every sequence holds the cache's length; with a mask whose
+  every row is a prefix (a static cache: its unused tail is masked) the
+  lengths are read from it once per forward (one host sync, shared by all
+  layers) and the kernels see the static buffers with per-sequence lengths;
+  any other mask (left padding) goes to SDPA.
 """
 from __future__ import annotations
 
@@ -28,6 +37,11 @@ except Exception:  # pragma: no cover - older transformers layouts
     from transformers.modeling_utils import AttentionInterface
 from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
 
+try:
+    from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, sdpa_mask
+except Exception:  # pragma: no cover - transformers without mask interfaces
+    ALL_MASK_ATTENTION_FUNCTIONS = sdpa_mask = None
+
 _ADAKV_CFG = dict(enabled=True, block_size=16, avg_budget=16, k_min=2, k_max=64,
                   n_sink_blocks=1, n_local_blocks=4, temperature=1.0,
                   estimator="centroid", budget_policy="adaptive",
@@ -39,17 +53,18 @@ _SDPA = ALL_ATTENTION_FUNCTIONS["sdpa"]
 
 class _LayerState:
     """Per-layer block summaries kept across decode steps: centroids
-    [B, Hkv, capacity_blocks, D] or minmax bounds [B, Hkv, capacity_blocks, 2*D]."""
+    [B, Hkv, capacity_blocks, D] or minmax bounds [B, Hkv, capacity_blocks, 2*D],
+    built from the first lens[b] tokens of sequence b."""
 
-    def __init__(self, key, block_size, centroid_dtype, estimator):
+    def __init__(self, key, block_size, centroid_dtype, estimator, lens, lens_dev):
         B, Hkv, S, D = key.shape
         nb = ops.n_blocks(S, block_size)
         cdt = _summary_dtype(key, centroid_dtype, estimator)
         self.sig = (B, Hkv, D, key.dtype, key.device, block_size, cdt, estimator)
         row = 2 * D if estimator == "minmax" else D
         self.centroid = torch.zeros(B, Hkv, nb + max(64, nb // 8), row, dtype=cdt, device=key.device)
-        ops.centroid_build(key, block_size, centroid=self.centroid, estimator=estimator)
-        self.seq_len = S
+        ops.centroid_build(key, block_size, seq_lens=lens_dev, centroid=self.centroid, estimator=estimator)
+        self.lens = list(lens)
 
     def grow(self, nb):
         if nb <= self.centroid.shape[2]:
@@ -63,6 +78,32 @@ class _LayerState:
 
 # Per-layer state keyed by id(module), like the reference's _FROZEN (patch.py:54).
 _STATE: dict[int, _LayerState] = {}
+
+# The lengths read from the last mask: (mask, result), so that the layers of
+# one forward, which share one mask object, read it once.
+_MASK_MEMO: list = [None, None]
+
+
+def _mask_lengths(mask, B, kv_len):
+    """(host lengths, device int32 lengths) when every row of the decode mask
+    (last query row) attends exactly a prefix of the keys, else None."""
+    if _MASK_MEMO[0] is mask:
+        return _MASK_MEMO[1]
+    res = None
+    if mask.dim() == 4 and mask.shape[-1] == kv_len and mask.shape[0] in (1, B):
+        m = mask[:, 0, -1, :]
+        if m.dtype != torch.bool:
+            m = m == 0                        # additive masks: 0 where attended
+        lens = m.sum(-1)
+        ok = (m == (torch.arange(kv_len, device=m.device)[None, :] < lens[:, None])).all()
+        host = torch.cat([lens, ok.view(1).to(lens.dtype)]).tolist()   # the one host sync
+        if host[-1] and min(host[:-1]) >= 1:
+            lens_h = [int(x) for x in host[:-1]]
+            if len(lens_h) == 1 and B > 1:
+                lens_h = lens_h * B
+            res = (lens_h, torch.tensor(lens_h, dtype=torch.int32, device=mask.device))
+    _MASK_MEMO[0], _MASK_MEMO[1] = mask, res
+    return res
 
 
 def _summary_dtype(key, centroid_dtype, estimator):
@@ -94,7 +135,7 @@ def adakv_attention_forward(module, query, key, value, attention_mask, scaling, 
     """
     cfg = _ADAKV_CFG
     B, Hq, q_len, D = query.shape
-    if (not cfg["enabled"]) or q_len != 1 or (B != 1 and attention_mask is not None):
+    if (not cfg["enabled"]) or q_len != 1:
         if q_len != 1:
             _STATE.pop(id(module), None)        # a new prefill starts a new sequence
         return _SDPA(module, query, key, value, attention_mask=attention_mask, scaling=scaling,
@@ -106,26 +147,40 @@ def adakv_attention_forward(module, query, key, value, attention_mask, scaling, 
         raise ValueError(f"unknown estimator: {cfg['estimator']!r}")
     bs = int(cfg["block_size"])
     S = key.shape[2]
+    if attention_mask is None:
+        lens, lens_dev = [S] * B, None
+    else:
+        got = _mask_lengths(attention_mask, B, S)
+        if got is None:                          # padding: not a prefix per row
+            return _SDPA(module, query, key, value, attention_mask=attention_mask, scaling=scaling,
+                         dropout=dropout, **kwargs)
+        lens, lens_dev = got
     st = _STATE.get(id(module))
-    if st is None or st.sig != _signature(key, cfg) or S < st.seq_len:
-        st = _LayerState(key, bs, cfg.get("centroid_dtype"), cfg["estimator"])
+    append_new = None
+    if st is not None and st.sig == _signature(key, cfg):
+        deltas = {n - p for n, p in zip(lens, st.lens)}
+        if len(deltas) == 1 and min(deltas) >= 0:
+            append_new = deltas.pop()
+    if append_new is None:                       # new sequence(s): build from the cache
+        st = _LayerState(key, bs, cfg.get("centroid_dtype"), cfg["estimator"], lens, lens_dev)
         _STATE[id(module)] = st
         append_new = 0
     else:
-        append_new = S - st.seq_len
         st.grow(ops.n_blocks(S, bs))
-        st.seq_len = S
+        st.lens = list(lens)
     out = torch.empty(B, 1, Hq, D, dtype=query.dtype, device=query.device)
     res = ops.decode_fused(query[:, :, 0, :], key, value, st.centroid, bs, _budget(cfg),
-                           append_new=append_new, sm_scale=scaling, out=out[:, 0],
+                           seq_lens=lens_dev, append_new=append_new, sm_scale=scaling, out=out[:, 0],
                            return_selection=instrumentation_active(), estimator=cfg["estimator"])
     if instrumentation_active():
-        _, table, lens = res
-        record_selection(table, lens, ops.n_blocks(S, bs))
+        _, table, sel = res
+        record_selection(table, sel, ops.n_blocks(max(lens), bs))
     return out, None
 
 
 AttentionInterface.register("adakv", adakv_attention_forward)
+if ALL_MASK_ATTENTION_FUNCTIONS is not None:
+    ALL_MASK_ATTENTION_FUNCTIONS.register("adakv", sdpa_mask)
 
 
 def install_adakv(model):

@@ -1,0 +1,141 @@
+"""The HuggingFace drop-in (adakv/patch.py:90-138) on the GPU: a small
+random-init Llama routed through ``patch_model``.
+
+* With a budget that selects every block, the sparse decode is attention over
+  the whole cache, so the patched model's decode logits must equal the
+  unpatched (SDPA) model's -- the reference's full-budget check
+  (tests/test_reference.py:71-79) at the model level, covering RoPE, GQA,
+  the softmax scale and the output layout.  fp32 (three-kernel path) and bf16
+  (fused path), centroid and minmax estimators, adaptive and nucleus budgets.
+* Dynamic and static caches, batch 1 and 2: the HIP path runs (the budget
+  trace records every layer of every step), with the static cache's lengths
+  taken from its mask.
+* A left-padded batch is not a prefix per row: the hook hands it to SDPA, so
+  the patched logits equal the unpatched ones exactly.
+* A normal budget: the realised mean budget is the requested one.
+"""
+from __future__ import annotations
+
+import pytest
+
+from gpu_util import DEV, need_gpu, say, torch
+
+pytestmark = pytest.mark.gpu
+
+VOCAB, PROMPT, STEPS = 256, 300, 4
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    need_gpu()
+
+
+def _model(dtype):
+    from transformers import LlamaConfig, LlamaForCausalLM
+    from adakv_amd.patch import install_adakv
+    cfg = LlamaConfig(vocab_size=VOCAB, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                      num_attention_heads=8, num_key_value_heads=2, head_dim=64,
+                      max_position_embeddings=4096)
+    torch.manual_seed(0)
+    m = LlamaForCausalLM(cfg).to(device=DEV, dtype=dtype).eval()
+    install_adakv(m)
+    return m
+
+
+FULL = dict(avg_budget=10 ** 6, k_min=10 ** 6, k_max=10 ** 6)
+
+
+def _cfg(**kw):
+    c = dict(block_size=16, avg_budget=8, k_min=2, k_max=64, n_sink_blocks=1, n_local_blocks=4,
+             temperature=1.0, estimator="centroid", budget_policy="adaptive", c_min=1, nucleus_p=0.9,
+             selection="adakv", centroid_dtype=None)
+    c.update(kw)
+    return c
+
+
+def _decode_logits(model, ids, cache_kind, attention_mask=None):
+    """Prefill `ids`, then STEPS single-token steps of fixed tokens; the logits of each step."""
+    from transformers import StaticCache
+    B = ids.shape[0]
+    cache = None
+    if cache_kind == "static":
+        cache = StaticCache(config=model.config, max_cache_len=PROMPT + STEPS + 37)
+    out = []
+    with torch.no_grad():
+        r = model(ids, attention_mask=attention_mask, past_key_values=cache, use_cache=True)
+        cache = r.past_key_values
+        am = attention_mask
+        for t in range(STEPS):
+            tok = torch.full((B, 1), (7 * t + 3) % VOCAB, dtype=torch.long, device=DEV)
+            if am is not None:
+                am = torch.cat([am, torch.ones(B, 1, dtype=am.dtype, device=DEV)], dim=1)
+            r = model(tok, attention_mask=am, past_key_values=cache, use_cache=True)
+            out.append(r.logits[:, -1].float())
+    return torch.stack(out)
+
+
+def _run(model, ids, cache_kind, cfg, attention_mask=None):
+    """(patched logits, unpatched logits, layer-steps recorded by the HIP path)."""
+    from adakv_amd import attention as A
+    from adakv_amd.patch import disable_adakv, enable_adakv
+    disable_adakv()
+    ref = _decode_logits(model, ids, cache_kind, attention_mask)
+    enable_adakv(**cfg)
+    A.reset_budget_trace()
+    got = _decode_logits(model, ids, cache_kind, attention_mask)
+    trace = A.get_budget_trace()
+    A.stop_budget_trace()
+    disable_adakv()
+    torch.cuda.synchronize()
+    return got, ref, trace
+
+
+def _ids(B):
+    g = torch.Generator().manual_seed(1)
+    return torch.randint(0, VOCAB, (B, PROMPT), generator=g).to(DEV)
+
+
+@pytest.mark.parametrize("cache_kind", ["dynamic", "static"])
+@pytest.mark.parametrize("B", [1, 2])
+def test_full_budget_equals_sdpa_fp32(cache_kind, B):
+    say(f"patch fp32 full budget, {cache_kind} cache, B={B}")
+    model = _model(torch.float32)
+    got, ref, trace = _run(model, _ids(B), cache_kind, _cfg(**FULL))
+    assert len(trace) == STEPS * 2, "the HIP path did not run on every layer of every step"
+    err = (got - ref).abs().max().item()
+    say(f"  max |logit diff| {err:.2e}")
+    assert err <= 2e-3 * max(ref.abs().max().item(), 1.0)
+
+
+@pytest.mark.parametrize("est,policy", [("centroid", "adaptive"), ("minmax", "fixed"),
+                                        ("centroid", "adaptive_nucleus")])
+@pytest.mark.parametrize("cache_kind", ["dynamic", "static"])
+def test_full_budget_equals_sdpa_bf16(cache_kind, est, policy):
+    say(f"patch bf16 full budget, {cache_kind} cache, {est}/{policy}")
+    model = _model(torch.bfloat16)
+    got, ref, trace = _run(model, _ids(2), cache_kind, _cfg(estimator=est, budget_policy=policy, **FULL))
+    assert len(trace) == STEPS * 2
+    rel = ((got - ref).norm() / ref.norm()).item()
+    say(f"  logits rel L2 {rel:.2e}")
+    assert rel < 2e-2
+
+
+def test_left_padded_batch_goes_to_sdpa():
+    say("patch left-padded batch -> SDPA")
+    model = _model(torch.bfloat16)
+    ids = _ids(2)
+    am = torch.ones(2, PROMPT, dtype=torch.long, device=DEV)
+    am[0, :17] = 0
+    got, ref, trace = _run(model, ids, "dynamic", _cfg(), attention_mask=am)
+    assert len(trace) == 0, "a padded batch must not take the sparse path"
+    assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("cache_kind", ["dynamic", "static"])
+def test_normal_budget_realises_the_mean(cache_kind):
+    say(f"patch bf16 avg_budget 8, {cache_kind} cache")
+    model = _model(torch.bfloat16)
+    got, ref, trace = _run(model, _ids(2), cache_kind, _cfg(avg_budget=8))
+    assert len(trace) == STEPS * 2
+    assert all(abs(t - 8.0) <= 0.5 for t in trace), trace
+    assert torch.isfinite(got).all()
