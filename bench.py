@@ -55,6 +55,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cells", action="store_true", help="skip the quest / adakv_cf / streaming legs")
+    ap.add_argument("--model-step", action="store_true",
+                    help="BASELINE config 5 instead: a Llama-3-70B-shaped 80-layer decode step through patch_model")
+    ap.add_argument("--model-layers", type=int, default=80)
+    ap.add_argument("--model-batch", type=int, default=4)
+    ap.add_argument("--model-ctx", type=int, default=65536)
     ap.add_argument("--seed", type=int, default=0)
     return ap.parse_args()
 
@@ -249,6 +254,130 @@ def cpu_baseline(torch, w: Workload, budget_s: float):
     return float(np.median(runs)), len(times)
 
 
+def model_step(args):
+    """Llama-3-70B-shaped decode (80 layers, hidden 8192, 64 q / 8 KV
+    heads, head_dim 128, MLP 28672, vocab 128256) with random-init bf16 weights, batch 4,
+    a 65536-token static KV cache synthesised directly (random bf16 K/V, no prefill),
+    through ``patch_model`` (block_size 16, avg_budget 8).  Per-token decode latency with
+    AdaKV, with a dense decode (this build's HIP flash-decode over every cached token, and
+    HF's SDPA, which expands K/V per layer under the static cache's mask), and with the
+    attention replaced by a no-op (which keeps the KV-cache write), so attention share
+    = 1 - t_noop / t."""
+    import torch
+    from transformers import AttentionInterface, LlamaConfig, LlamaForCausalLM, StaticCache
+    from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, sdpa_mask
+
+    from adakv_amd import ops
+    from adakv_amd import patch as P
+    dev = torch.device("cuda:0")
+    L, B, S0 = args.model_layers, args.model_batch, args.model_ctx
+    cfg = LlamaConfig(vocab_size=128256, hidden_size=8192, intermediate_size=28672, num_hidden_layers=L,
+                      num_attention_heads=64, num_key_value_heads=8, head_dim=128,
+                      max_position_embeddings=131072, rope_theta=500000.0, tie_word_embeddings=False)
+    log(f"model step: {L} layers, batch {B}, ctx {S0}: building random-init bf16 weights on the GPU")
+    with torch.device("meta"):
+        model = LlamaForCausalLM(cfg)
+    model = model.to(torch.bfloat16).to_empty(device=dev)        # bf16 before any memory exists
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    for i, (name, p) in enumerate(model.named_parameters()):
+        with torch.no_grad():
+            if name.endswith("norm.weight"):
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, 0.02, generator=gen)
+        if i % 9 == 0:
+            log(f"  initialised {i} parameter tensors ({name})")
+    # the rotary table is a non-persistent buffer: rebuild it on the device
+    model.model.rotary_emb = type(model.model.rotary_emb)(config=cfg).to(dev)
+    model.eval()
+    P.install_adakv(model)
+    n_params = sum(p.numel() for p in model.parameters())
+    steps, warm = max(args.steps // 64, 4), 2
+    cache = StaticCache(config=cfg, max_cache_len=S0 + 4 * (steps + warm) + 16)
+    kd = torch.zeros(B, 8, 1, 128, dtype=torch.bfloat16, device=dev)
+    for i, layer in enumerate(cache.layers):
+        layer.lazy_initialization(kd, kd)
+        layer.keys[:, :, :S0].normal_(generator=gen)
+        layer.values[:, :, :S0].normal_(generator=gen)
+        if isinstance(layer.cumulative_length, torch.Tensor):
+            layer.cumulative_length.fill_(S0)
+        else:
+            layer.cumulative_length = S0
+        if i % 4 == 0:
+            log(f"  KV cache layer {i} filled")
+    torch.cuda.synchronize()
+    log(f"  {n_params / 1e9:.1f} B parameters, {torch.cuda.memory_allocated() / 2**30:.0f} GiB allocated")
+
+    def noop_attention(module, query, key, value, attention_mask, scaling, dropout=0.0, **kw):
+        Bq, Hq, q_len, D = query.shape
+        return query.new_zeros(Bq, q_len, Hq, D), None
+
+    def dense_hip_attention(module, query, key, value, attention_mask, scaling, dropout=0.0, **kw):
+        Bq, Hq, q_len, D = query.shape
+        lens = None if attention_mask is None else P._mask_lengths(attention_mask, Bq, key.shape[2])
+        out = torch.empty(Bq, 1, Hq, D, dtype=query.dtype, device=query.device)
+        ops.dense_decode(query[:, :, 0, :], key, value, sm_scale=scaling,
+                         seq_lens=None if lens is None else lens[1], out=out[:, 0])
+        return out, None
+
+    AttentionInterface.register("adakv_noop", noop_attention)
+    ALL_MASK_ATTENTION_FUNCTIONS.register("adakv_noop", sdpa_mask)
+    AttentionInterface.register("adakv_dense_hip", dense_hip_attention)
+    ALL_MASK_ATTENTION_FUNCTIONS.register("adakv_dense_hip", sdpa_mask)
+    pos = [S0]
+
+    def one_step():
+        tok = torch.randint(0, cfg.vocab_size, (B, 1), device=dev, generator=gen)
+        pid = torch.full((B, 1), pos[0], dtype=torch.long, device=dev)
+        with torch.no_grad():
+            model(input_ids=tok, position_ids=pid, past_key_values=cache, use_cache=True)
+        pos[0] += 1
+
+    def timed(label):
+        for _ in range(warm):
+            one_step()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(steps):
+            one_step()
+        e.record()
+        torch.cuda.synchronize()
+        ms = s.elapsed_time(e) / steps
+        log(f"  {label}: {ms:.2f} ms/token")
+        return ms
+
+    P.enable_adakv(block_size=16, avg_budget=8, k_min=2, k_max=64, n_sink_blocks=1, n_local_blocks=4,
+                   temperature=1.0, estimator="centroid", budget_policy="adaptive", c_min=1)
+    t_adakv = timed("adakv (patch_model, avg_budget 8)")
+    P.disable_adakv()
+    t_dense = timed("dense (HF SDPA)")
+    model.set_attn_implementation("adakv_dense_hip")
+    t_dense_hip = timed("dense (HIP flash-decode)")
+    model.set_attn_implementation("adakv_noop")
+    t_noop = timed("attention replaced by a no-op")
+    P.install_adakv(model)
+    res = {
+        "metric": "70B-shaped decode step ms/token (BASELINE config 5), 1 MI355X", "value": round(t_adakv, 3),
+        "unit": "ms/token", "n_gpus": 1, "steps": steps, "warmup": warm, "higher_is_better": False,
+        "dtype": "bf16", "data": "synthetic (random-init weights, random K/V cache)",
+        "config": {"workload": "Llama-3-70B-shaped decode step via patch_model (BASELINE config 5)",
+                   "layers": L, "batch": B, "context": S0, "n_q_heads": 64, "n_kv_heads": 8, "head_dim": 128,
+                   "hidden": 8192, "block_size": 16, "avg_budget": 8, "cache": "StaticCache",
+                   "parameters": n_params},
+        "dense_hip_ms_per_token": round(t_dense_hip, 3), "dense_sdpa_ms_per_token": round(t_dense, 3),
+        "noop_attention_ms_per_token": round(t_noop, 3),
+        "attention_share_adakv": round(max(t_adakv - t_noop, 0.0) / t_adakv, 4),
+        "attention_share_dense_hip": round(max(t_dense_hip - t_noop, 0.0) / t_dense_hip, 4),
+        "attention_share_dense_sdpa": round(max(t_dense - t_noop, 0.0) / t_dense, 4),
+        "adakv_attention_us_per_layer": round(max(t_adakv - t_noop, 0.0) * 1e3 / L, 2),
+        "dense_hip_attention_us_per_layer": round(max(t_dense_hip - t_noop, 0.0) * 1e3 / L, 2),
+        "speedup_vs_dense_hip_step": round(t_dense_hip / t_adakv, 3),
+        "speedup_vs_dense_sdpa_step": round(t_dense / t_adakv, 3),
+    }
+    print(json.dumps(res), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -261,6 +390,9 @@ def main():
     from adakv_amd import _capi, ops
     _capi.load()
     assert torch.cuda.is_available(), "bench.py needs a ROCm device"
+    if args.model_step:
+        model_step(args)
+        return
     log(f"device {torch.cuda.get_device_name(0)}; building {args.layers} layers at ctx {args.ctx}")
     w = Workload(torch, ops, args.ctx, args.layers, args.avg_budget, args.seed)
     L = w.L
