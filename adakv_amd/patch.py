@@ -127,11 +127,15 @@ def _budget(cfg):
                             nucleus_p=cfg.get("nucleus_p", 0.9))
 
 
+@torch.compiler.disable
 def adakv_attention_forward(module, query, key, value, attention_mask, scaling, dropout=0.0,
                             **kwargs):
     """HF attention function (adakv/patch.py:90-121).
 
     query [B, Hq, q_len, D], key/value [B, Hkv, S, D] -> ([B, q_len, Hq, D], None).
+    Excluded from torch.compile tracing (HF compiles the decode step of static
+    caches): it launches through ctypes and keeps per-layer host state, so a
+    compiled graph calls it as an opaque step.
     """
     cfg = _ADAKV_CFG
     B, Hq, q_len, D = query.shape

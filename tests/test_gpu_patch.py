@@ -139,3 +139,33 @@ def test_normal_budget_realises_the_mean(cache_kind):
     assert len(trace) == STEPS * 2
     assert all(abs(t - 8.0) <= 0.5 for t in trace), trace
     assert torch.isfinite(got).all()
+
+
+def test_generate_with_static_cache_matches_sdpa_greedy():
+    """model.generate with an HF StaticCache (the usage INTEGRATION.md shows):
+    with a budget that selects every block the greedy continuation equals the
+    unpatched model's, and every decode step ran on the HIP path."""
+    from transformers import StaticCache
+    from adakv_amd import attention as A
+    from adakv_amd.patch import disable_adakv, enable_adakv
+    say("patch generate() with StaticCache, fp32, full budget")
+    model = _model(torch.float32)
+    ids = _ids(2)
+    new = 6
+
+    def gen():
+        cache = StaticCache(config=model.config, max_cache_len=PROMPT + new + 40)
+        with torch.no_grad():
+            return model.generate(ids, attention_mask=torch.ones_like(ids), past_key_values=cache,
+                                  max_new_tokens=new, do_sample=False, pad_token_id=0)
+
+    disable_adakv()
+    ref = gen()
+    enable_adakv(**_cfg(**FULL))
+    A.reset_budget_trace()
+    got = gen()
+    trace = A.get_budget_trace()
+    A.stop_budget_trace()
+    disable_adakv()
+    assert len(trace) == (new - 1) * 2, f"{len(trace)} layer-steps on the HIP path"
+    assert torch.equal(got, ref)
