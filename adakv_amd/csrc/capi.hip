@@ -18,7 +18,8 @@ constexpr int kMaxBlocks = 32768;
 constexpr int kMaxSparseSplits = 16;      // the in-kernel merge reads at most 16 partials
 constexpr int kSparseMinPer = 32;         // blocks a sparse split takes at least
 constexpr int kMaxDenseSplits = 256;
-constexpr int kDenseBlocksPerSplit = 128;
+constexpr int kDenseMinBlocksPerSplit = 8;
+constexpr int kDenseTargetGroups = 512;   // dense workgroups to aim for: two per CU
 constexpr size_t kLdsLimit = 65536;
 constexpr int kMaxPlanCounters = 4096;                  // one per sequence
 constexpr int kMaxDecodeCounters = 12288;               // one per (sequence, KV head)
@@ -321,7 +322,11 @@ WorkspaceLayout workspace_layout(const adakv_geometry_t& g, int T) {
   const int64_t umax = union_max(g, T);
   L.nsplit_sparse = (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div_h(umax, kSparseMinPer),
                                                                 kMaxSparseSplits));
-  L.nsplit_dense = std::max(1, std::min(ceil_div_h(g.max_blocks, kDenseBlocksPerSplit), kMaxDenseSplits));
+  // dense splits: about kDenseTargetGroups workgroups over the (sequence, KV head)
+  // pairs, at least kDenseMinBlocksPerSplit blocks each
+  L.nsplit_dense = std::max(1, std::min({ceil_div_h(g.max_blocks, kDenseMinBlocksPerSplit),
+                                         ceil_div_h(kDenseTargetGroups, (int64_t)g.batch * g.n_kv_heads),
+                                         kMaxDenseSplits}));
   L.nsplit_max = std::max(L.nsplit_sparse, L.nsplit_dense);
   // The counters sit at fixed offsets so that they stay zero however the
   // geometry of successive calls on one workspace changes; everything after

@@ -55,6 +55,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cells", action="store_true", help="skip the quest / adakv_cf / streaming legs")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the context sweep")
+    ap.add_argument("--sweep-ctx", type=str, default="4096,16384,32768,65536,262144")
     ap.add_argument("--model-step", action="store_true",
                     help="BASELINE config 5 instead: a Llama-3-70B-shaped 80-layer decode step through patch_model")
     ap.add_argument("--model-layers", type=int, default=80)
@@ -462,6 +464,26 @@ def main():
             cells["dense"] = {"us_per_layer": round(dense_us, 2), "estimator": None,
                               "budget_policy": None, "summary_bytes_per_layer": 0}
 
+    sweep = None
+    if not args.no_sweep:
+        # latency against context (the reference's efficiency experiment,
+        # bench_decode_latency.py:1-24): the same layer shape, 8 rotated layers
+        # per context, AdaKV step and dense decode
+        sweep = []
+        for ctx in [int(x) for x in args.sweep_ctx.split(",") if x]:
+            ws = Workload(torch, ops, ctx, 8, args.avg_budget, args.seed + 1)
+            g1 = capture(torch, ws.step, ws.L, stream)
+            ms1, _ = time_graph(torch, g1, 16, 2)
+            g2 = capture(torch, ws.dense, ws.L, stream)
+            ms2, _ = time_graph(torch, g2, 4, 1)
+            a_us, d_us = ms1 * 1e3 / (16 * ws.L), ms2 * 1e3 / (4 * ws.L)
+            sweep.append({"context": ctx, "adakv_us_per_layer": round(a_us, 2),
+                          "dense_us_per_layer": round(d_us, 2), "speedup": round(d_us / a_us, 2),
+                          "path": "fused (2 launches)" if ws.nb <= 8192 else "plan + decode (3 launches)"})
+            log(f"ctx {ctx}: adakv {a_us:.2f} us/layer, dense {d_us:.2f} us/layer")
+            del g1, g2, ws
+            torch.cuda.empty_cache()
+
     cpu = None
     if not args.no_cpu:
         sec, runs = cpu_baseline(torch, w, args.cpu_seconds)
@@ -497,6 +519,7 @@ def main():
                      "frac_of_stream_copy": round(sc_gbps / copy_gbps, 4)},
         "cpu_baseline": cpu,
         "cells": cells,
+        "ctx_sweep": sweep,
     }
     print(json.dumps(res), flush=True)
 
