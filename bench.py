@@ -56,6 +56,7 @@ def parse():
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cells", action="store_true", help="skip the quest / adakv_cf / streaming legs")
     ap.add_argument("--no-sweep", action="store_true", help="skip the context sweep")
+    ap.add_argument("--no-ragged", action="store_true", help="skip the ragged-batch leg (BASELINE config 4)")
     ap.add_argument("--sweep-ctx", type=str, default="4096,16384,32768,65536,262144")
     ap.add_argument("--model-step", action="store_true",
                     help="BASELINE config 5 instead: a Llama-3-70B-shaped 80-layer decode step through patch_model")
@@ -200,6 +201,48 @@ def selection_bytes(torch, ops, w: Workload):
     b_meta = w.Hq * T * 4 * 2 + w.Hq * 4 * 2 + w.Hkv * (w.BS * w.D * e + w.D * e)
     return dict(centroid=b_cent, kv=b_kv, q=b_q, out=b_out, meta=b_meta,
                 total=b_cent + b_kv + b_q + b_out + b_meta, union_blocks_per_layer=u)
+
+
+def ragged_batch(torch, ops, stream, seed, layers=4):
+    """8 sequences with lengths uniform in [16K, 128K] (fixed
+    seed), 32 q / 8 KV heads, head_dim 128, bf16, block_size 16, avg_budget 16;
+    half the KV heads peaked (keys x4).  One step decodes the whole batch
+    (per-sequence lengths on the device); 4 layers' buffers rotate."""
+    B, Hq, Hkv, D, BS, cap = 8, 32, 8, 128, 16, 131072
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    lens = torch.randint(16384, cap + 1, (B,), generator=torch.Generator().manual_seed(seed)).to(torch.int32)
+    sl = lens.to(dev)
+    budget = ops.BudgetParams(avg_budget=16)
+    L = []
+    for _ in range(layers):
+        k = torch.randn(B, Hkv, cap, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        k[:, : Hkv // 2] *= 4.0
+        v = torch.randn(B, Hkv, cap, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        q = torch.randn(B, Hq, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        c = ops.centroid_build(k, BS, seq_lens=sl)
+        L.append((q, k, v, c, torch.empty_like(q)))
+    torch.cuda.synchronize()
+
+    def step(l):
+        q, k, v, c, o = L[l]
+        ops.decode_fused(q, k, v, c, BS, budget, seq_lens=sl, append_new=1, out=o)
+
+    def dense(l):
+        q, k, v, _, o = L[l]
+        ops.dense_decode(q, k, v, seq_lens=sl, out=o)
+
+    g1 = capture(torch, step, layers, stream)
+    ms1, _ = time_graph(torch, g1, 40, 2)
+    g2 = capture(torch, dense, layers, stream)
+    ms2, _ = time_graph(torch, g2, 10, 1)
+    a_us, d_us = ms1 * 1e3 / (40 * layers), ms2 * 1e3 / (10 * layers)
+    kv_dense = int(lens.sum()) * Hkv * D * 2 * 2
+    log(f"ragged batch (config 4, lengths {lens.tolist()}): adakv {a_us:.2f} us/step, dense {d_us:.2f} us/step")
+    return {"config": "BASELINE config 4: 8 sequences, lengths uniform in [16K, 128K], avg_budget 16",
+            "lengths": lens.tolist(), "adakv_us_per_layer_step": round(a_us, 2),
+            "dense_us_per_layer_step": round(d_us, 2), "speedup": round(d_us / a_us, 2),
+            "dense_GBps": round(kv_dense / (d_us * 1e-6) / 1e9, 1)}
 
 
 def stream_copy_gbps(torch, nbytes: int = 1 << 30, reps: int = 10) -> float:
@@ -484,6 +527,10 @@ def main():
             del g1, g2, ws
             torch.cuda.empty_cache()
 
+    ragged = None
+    if not args.no_ragged:
+        ragged = ragged_batch(torch, ops, stream, args.seed + 2)
+
     cpu = None
     if not args.no_cpu:
         sec, runs = cpu_baseline(torch, w, args.cpu_seconds)
@@ -520,6 +567,7 @@ def main():
         "cpu_baseline": cpu,
         "cells": cells,
         "ctx_sweep": sweep,
+        "ragged_batch": ragged,
     }
     print(json.dumps(res), flush=True)
 
