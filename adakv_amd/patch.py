@@ -18,11 +18,14 @@ policy.  Differences from the reference hook (patch.py:90-121):
   only the blocks that gained tokens (the reference rebuilds them from the
   whole cache every step, patch.py:110);
 * batches of any size decode sparsely.  With no mask (a dynamic cache and an
-  unpadded batch) every sequence holds the cache's length; with a mask whose
-  every row is a prefix (a static cache: its unused tail is masked) the
-  lengths are read from it once per forward (one host sync, shared by all
-  layers) and the kernels see the static buffers with per-sequence lengths;
-  any other mask (left padding) goes to SDPA.
+  unpadded batch) every sequence holds the cache's length.  Otherwise each
+  row of the decode mask must attend one contiguous run of keys, read from it
+  once per forward (one host sync, shared by all layers): runs that all start
+  at 0 (a static cache, whose unused tail is masked) decode as one batch with
+  per-sequence lengths; runs that start later (left padding) decode one
+  sequence at a time on its own view of the cache, so that its blocks count
+  from its first real token, as for an unpadded sequence.  Any other mask goes
+  to SDPA.
 """
 from __future__ import annotations
 
@@ -54,16 +57,22 @@ _SDPA = ALL_ATTENTION_FUNCTIONS["sdpa"]
 class _LayerState:
     """Per-layer block summaries kept across decode steps: centroids
     [B, Hkv, capacity_blocks, D] or minmax bounds [B, Hkv, capacity_blocks, 2*D],
-    built from the first lens[b] tokens of sequence b."""
+    built from tokens [starts[b], starts[b] + lens[b]) of sequence b."""
 
-    def __init__(self, key, block_size, centroid_dtype, estimator, lens, lens_dev):
+    def __init__(self, key, block_size, centroid_dtype, estimator, starts, lens, lens_dev):
         B, Hkv, S, D = key.shape
         nb = ops.n_blocks(S, block_size)
         cdt = _summary_dtype(key, centroid_dtype, estimator)
         self.sig = (B, Hkv, D, key.dtype, key.device, block_size, cdt, estimator)
         row = 2 * D if estimator == "minmax" else D
         self.centroid = torch.zeros(B, Hkv, nb + max(64, nb // 8), row, dtype=cdt, device=key.device)
-        ops.centroid_build(key, block_size, seq_lens=lens_dev, centroid=self.centroid, estimator=estimator)
+        if not any(starts):
+            ops.centroid_build(key, block_size, seq_lens=lens_dev, centroid=self.centroid, estimator=estimator)
+        else:
+            for b in range(B):
+                ops.centroid_build(key[b:b + 1, :, starts[b]:starts[b] + lens[b]], block_size,
+                                   centroid=self.centroid[b:b + 1], estimator=estimator)
+        self.starts = list(starts)
         self.lens = list(lens)
 
     def grow(self, nb):
@@ -79,14 +88,15 @@ class _LayerState:
 # Per-layer state keyed by id(module), like the reference's _FROZEN (patch.py:54).
 _STATE: dict[int, _LayerState] = {}
 
-# The lengths read from the last mask: (mask, result), so that the layers of
-# one forward, which share one mask object, read it once.
+# The runs read from the last mask: (mask, result), so that the layers of one
+# forward, which share one mask object, read it once.
 _MASK_MEMO: list = [None, None]
 
 
-def _mask_lengths(mask, B, kv_len):
-    """(host lengths, device int32 lengths) when every row of the decode mask
-    (last query row) attends exactly a prefix of the keys, else None."""
+def _mask_runs(mask, B, kv_len):
+    """(host starts, host lengths, device int32 lengths) when every row of the
+    decode mask (its last query row) attends one non-empty contiguous run of
+    keys [start, start + length), else None."""
     if _MASK_MEMO[0] is mask:
         return _MASK_MEMO[1]
     res = None
@@ -95,13 +105,16 @@ def _mask_lengths(mask, B, kv_len):
         if m.dtype != torch.bool:
             m = m == 0                        # additive masks: 0 where attended
         lens = m.sum(-1)
-        ok = (m == (torch.arange(kv_len, device=m.device)[None, :] < lens[:, None])).all()
-        host = torch.cat([lens, ok.view(1).to(lens.dtype)]).tolist()   # the one host sync
-        if host[-1] and min(host[:-1]) >= 1:
-            lens_h = [int(x) for x in host[:-1]]
-            if len(lens_h) == 1 and B > 1:
-                lens_h = lens_h * B
-            res = (lens_h, torch.tensor(lens_h, dtype=torch.int32, device=mask.device))
+        first = torch.argmax(m.to(torch.uint8), dim=-1)
+        pos = torch.arange(kv_len, device=m.device)[None, :]
+        ok = (m == ((pos >= first[:, None]) & (pos < (first + lens)[:, None]))).all()
+        host = torch.cat([lens, first.to(lens.dtype), ok.view(1).to(lens.dtype)]).tolist()   # one host sync
+        n = m.shape[0]
+        lens_h, starts_h = [int(x) for x in host[:n]], [int(x) for x in host[n:2 * n]]
+        if host[-1] and min(lens_h) >= 1:
+            if n == 1 and B > 1:
+                lens_h, starts_h = lens_h * B, starts_h * B
+            res = (starts_h, lens_h, torch.tensor(lens_h, dtype=torch.int32, device=mask.device))
     _MASK_MEMO[0], _MASK_MEMO[1] = mask, res
     return res
 
@@ -152,33 +165,42 @@ def adakv_attention_forward(module, query, key, value, attention_mask, scaling, 
     bs = int(cfg["block_size"])
     S = key.shape[2]
     if attention_mask is None:
-        lens, lens_dev = [S] * B, None
+        starts, lens, lens_dev = [0] * B, [S] * B, None
     else:
-        got = _mask_lengths(attention_mask, B, S)
-        if got is None:                          # padding: not a prefix per row
+        got = _mask_runs(attention_mask, B, S)
+        if got is None:                          # not one contiguous run per row
             return _SDPA(module, query, key, value, attention_mask=attention_mask, scaling=scaling,
                          dropout=dropout, **kwargs)
-        lens, lens_dev = got
+        starts, lens, lens_dev = got
     st = _STATE.get(id(module))
     append_new = None
-    if st is not None and st.sig == _signature(key, cfg):
+    if st is not None and st.sig == _signature(key, cfg) and st.starts == starts:
         deltas = {n - p for n, p in zip(lens, st.lens)}
         if len(deltas) == 1 and min(deltas) >= 0:
             append_new = deltas.pop()
     if append_new is None:                       # new sequence(s): build from the cache
-        st = _LayerState(key, bs, cfg.get("centroid_dtype"), cfg["estimator"], lens, lens_dev)
+        st = _LayerState(key, bs, cfg.get("centroid_dtype"), cfg["estimator"], starts, lens, lens_dev)
         _STATE[id(module)] = st
         append_new = 0
     else:
         st.grow(ops.n_blocks(S, bs))
         st.lens = list(lens)
     out = torch.empty(B, 1, Hq, D, dtype=query.dtype, device=query.device)
-    res = ops.decode_fused(query[:, :, 0, :], key, value, st.centroid, bs, _budget(cfg),
-                           seq_lens=lens_dev, append_new=append_new, sm_scale=scaling, out=out[:, 0],
-                           return_selection=instrumentation_active(), estimator=cfg["estimator"])
-    if instrumentation_active():
-        _, table, sel = res
-        record_selection(table, sel, ops.n_blocks(max(lens), bs))
+    want = instrumentation_active()
+    budget = _budget(cfg)
+    if not any(starts):
+        res = [ops.decode_fused(query[:, :, 0, :], key, value, st.centroid, bs, budget, seq_lens=lens_dev,
+                                append_new=append_new, sm_scale=scaling, out=out[:, 0],
+                                return_selection=want, estimator=cfg["estimator"])]
+    else:
+        # left padding: each sequence on its own view, tokens [start, start + length)
+        res = [ops.decode_fused(query[b:b + 1, :, 0, :], key[b:b + 1, :, starts[b]:starts[b] + lens[b]],
+                                value[b:b + 1, :, starts[b]:starts[b] + lens[b]], st.centroid[b:b + 1], bs,
+                                budget, append_new=append_new, sm_scale=scaling, out=out[b:b + 1, 0],
+                                return_selection=want, estimator=cfg["estimator"]) for b in range(B)]
+    if want:
+        record_selection(torch.cat([r[1] for r in res]), torch.cat([r[2] for r in res]),
+                         ops.n_blocks(max(lens), bs))
     return out, None
 
 

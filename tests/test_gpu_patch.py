@@ -10,8 +10,10 @@ random-init Llama routed through ``patch_model``.
 * Dynamic and static caches, batch 1 and 2: the HIP path runs (the budget
   trace records every layer of every step), with the static cache's lengths
   taken from its mask.
-* A left-padded batch is not a prefix per row: the hook hands it to SDPA, so
-  the patched logits equal the unpatched ones exactly.
+* A left-padded batch (each mask row one contiguous run that starts late):
+  every sequence decodes on its own view of the cache, blocks counted from its
+  first real token; with every block selected it equals SDPA over the mask.
+* A mask row that is not one contiguous run goes to SDPA.
 * A normal budget: the realised mean budget is the requested one.
 """
 from __future__ import annotations
@@ -120,14 +122,41 @@ def test_full_budget_equals_sdpa_bf16(cache_kind, est, policy):
     assert rel < 2e-2
 
 
-def test_left_padded_batch_goes_to_sdpa():
-    say("patch left-padded batch -> SDPA")
-    model = _model(torch.bfloat16)
-    ids = _ids(2)
-    am = torch.ones(2, PROMPT, dtype=torch.long, device=DEV)
+def _left_padded(B=3):
+    am = torch.ones(B, PROMPT, dtype=torch.long, device=DEV)
     am[0, :17] = 0
-    got, ref, trace = _run(model, ids, "dynamic", _cfg(), attention_mask=am)
-    assert len(trace) == 0, "a padded batch must not take the sparse path"
+    am[2, :40] = 0
+    return am
+
+
+@pytest.mark.parametrize("cache_kind", ["dynamic", "static"])
+def test_left_padded_batch_full_budget_equals_sdpa(cache_kind):
+    say(f"patch left-padded batch of 3, fp32 full budget, {cache_kind} cache")
+    model = _model(torch.float32)
+    got, ref, trace = _run(model, _ids(3), cache_kind, _cfg(**FULL), attention_mask=_left_padded())
+    assert len(trace) == STEPS * 2, "the HIP path did not run on every layer of every step"
+    err = (got - ref).abs().max().item()
+    say(f"  max |logit diff| {err:.2e}")
+    assert err <= 2e-3 * max(ref.abs().max().item(), 1.0)
+
+
+def test_left_padded_batch_bf16_normal_budget():
+    say("patch left-padded batch of 3, bf16, avg_budget 8")
+    model = _model(torch.bfloat16)
+    got, ref, trace = _run(model, _ids(3), "dynamic", _cfg(avg_budget=8), attention_mask=_left_padded())
+    assert len(trace) == STEPS * 2
+    assert all(abs(t - 8.0) <= 0.5 for t in trace), trace
+    assert torch.isfinite(got).all()
+
+
+def test_non_contiguous_mask_goes_to_sdpa():
+    """A mask row with a hole is not one run: the hook hands the step to SDPA."""
+    say("patch mask with a hole -> SDPA")
+    model = _model(torch.bfloat16)
+    am = torch.ones(2, PROMPT, dtype=torch.long, device=DEV)
+    am[1, 100:110] = 0
+    got, ref, trace = _run(model, _ids(2), "dynamic", _cfg(), attention_mask=am)
+    assert len(trace) == 0, "a mask with a hole must not take the sparse path"
     assert torch.equal(got, ref)
 
 
