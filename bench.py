@@ -359,10 +359,12 @@ def model_step(args):
 
     def dense_hip_attention(module, query, key, value, attention_mask, scaling, dropout=0.0, **kw):
         Bq, Hq, q_len, D = query.shape
-        lens = None if attention_mask is None else P._mask_lengths(attention_mask, Bq, key.shape[2])
+        runs = None if attention_mask is None else P._mask_runs(attention_mask, Bq, key.shape[2])
+        if attention_mask is not None and (runs is None or any(runs[0])):
+            raise RuntimeError("dense HIP leg: the static cache's mask is not a prefix per sequence")
         out = torch.empty(Bq, 1, Hq, D, dtype=query.dtype, device=query.device)
         ops.dense_decode(query[:, :, 0, :], key, value, sm_scale=scaling,
-                         seq_lens=None if lens is None else lens[1], out=out[:, 0])
+                         seq_lens=None if runs is None else runs[2], out=out[:, 0])
         return out, None
 
     AttentionInterface.register("adakv_noop", noop_attention)
