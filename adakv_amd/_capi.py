@@ -27,7 +27,7 @@ ADAKV_ERR_VALUE = 7
 ADAKV_F32, ADAKV_F16, ADAKV_BF16 = 0, 1, 2
 POLICY_FIXED, POLICY_ADAPTIVE, POLICY_NUCLEUS = 0, 1, 2
 SUMMARY_CENTROID, SUMMARY_MINMAX = 0, 1
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class Geometry(ctypes.Structure):
@@ -65,6 +65,13 @@ class Selection(ctypes.Structure):
     _fields_ = [("block_table", c_void_p), ("table_width", c_int32), ("sel_lens", c_void_p)]
 
 
+class Prompt(ctypes.Structure):
+    _fields_ = [("q", c_void_p), ("k", c_void_p), ("dtype", c_int32), ("n_q_heads", c_int32),
+                ("n_kv_heads", c_int32), ("head_dim", c_int32), ("n_tokens", c_int32),
+                ("q_stride_h", ctypes.c_int64), ("q_stride_s", ctypes.c_int64),
+                ("k_stride_h", ctypes.c_int64), ("k_stride_s", ctypes.c_int64)]
+
+
 P = ctypes.POINTER
 SIGNATURES = {
     "adakv_status_string": (ctypes.c_char_p, [ctypes.c_int]),
@@ -86,6 +93,17 @@ SIGNATURES = {
                                           P(Output), c_void_p, ctypes.c_size_t, c_void_p]),
     "adakv_dense_decode": (ctypes.c_int, [P(Geometry), P(Query), P(KV), c_void_p, ctypes.c_float,
                                           P(Output), c_void_p, ctypes.c_size_t, c_void_p]),
+    "adakv_importance_workspace_bytes": (ctypes.c_size_t, [P(Prompt), c_int32]),
+    "adakv_key_importance": (ctypes.c_int, [P(Prompt), c_int32, ctypes.c_float, c_void_p, c_int32,
+                                            c_void_p, ctypes.c_size_t, c_void_p]),
+    "adakv_importance_pool": (ctypes.c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
+                                             c_void_p]),
+    "adakv_retain_blocks": (ctypes.c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+                                           c_int32, c_int32, c_void_p, c_int32, P(Selection), c_void_p]),
+    "adakv_frozen_table": (ctypes.c_int, [P(Selection), c_int32, c_int32, c_int32, c_int32, c_int32,
+                                          P(Selection), c_void_p]),
+    "adakv_mask_table": (ctypes.c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+                                        P(Selection), c_void_p]),
 }
 
 _LIB = None

@@ -21,7 +21,7 @@ INCLUDE = os.path.join(ROOT, "include")
 OUT_DIR = os.path.join(PKG, "_lib")
 BUILD_DIR = os.path.join(PKG, "_build")
 LIB_NAME = "libadakv_amd.so"
-SOURCES = ["centroid.hip", "plan.hip", "minmax.hip", "decode.hip", "fused.hip", "capi.hip"]
+SOURCES = ["centroid.hip", "plan.hip", "minmax.hip", "decode.hip", "fused.hip", "evict.hip", "capi.hip"]
 ARCH = os.environ.get("ADAKV_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [

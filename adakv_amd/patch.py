@@ -26,11 +26,21 @@ policy.  Differences from the reference hook (patch.py:90-121):
   sequence at a time on its own view of the cache, so that its blocks count
   from its first real token, as for an unpadded sequence.  Any other mask goes
   to SDPA.
+
+``selection="h2o"`` / ``"snapkv"`` selects the eviction baselines
+(patch.py:57-87): on a single-sequence prefill that holds the whole prompt,
+each layer freezes its retained block set from the prompt's attention (HIP
+importance + retention; the prefill output itself is SDPA's), and each decode
+step attends that set plus the current sink and local blocks through the
+table-driven sparse decode.  As in the reference, batches of more than one
+sequence go to SDPA, and a layer whose prefill was not seen attends every
+block.
 """
 from __future__ import annotations
 
 import torch
 
+from . import baselines_rt as _brt
 from . import ops
 from .attention import instrumentation_active, record_selection
 
@@ -88,6 +98,20 @@ class _LayerState:
 # Per-layer state keyed by id(module), like the reference's _FROZEN (patch.py:54).
 _STATE: dict[int, _LayerState] = {}
 
+class _Frozen:
+    """A layer's retained set, frozen at prefill: mask [Hq, nbp] bool and the
+    same blocks as an ascending table [Hq, k] with lens [Hq]."""
+
+    def __init__(self, mask, table, lens, nbp):
+        self.mask, self.table, self.lens, self.nbp = mask, table, lens, nbp
+
+
+# Eviction baselines' frozen sets keyed by id(module) (the reference's _FROZEN,
+# patch.py:51-54); refreshed by every prefill, cleared by enable_adakv.
+_FROZEN: dict[int, _Frozen] = {}
+_ALL_BLOCKS: dict = {}
+
+
 # The runs read from the last mask: (mask, result), so that the layers of one
 # forward, which share one mask object, read it once.
 _MASK_MEMO: list = [None, None]
@@ -140,6 +164,70 @@ def _budget(cfg):
                             nucleus_p=cfg.get("nucleus_p", 0.9))
 
 
+def _prompt_len(key, attention_mask):
+    """Tokens of the single sequence a forward sees: the mask's run when there
+    is a mask (a static cache's unused tail is masked), else the key length.
+    None when the mask row is not one run from position 0."""
+    if attention_mask is None:
+        return key.shape[2], None
+    got = _mask_runs(attention_mask, 1, key.shape[2])
+    if got is None or got[0][0] != 0:
+        return None, None
+    return got[1][0], got[2]
+
+
+def _capture_frozen(module, query, key, attention_mask, cfg, sel):
+    """Freeze this layer's retained blocks from the prompt (patch.py:57-73):
+    per-q-head importance of the prompt's keys (H2O: every prompt query;
+    SnapKV: the last obs_window queries, max-pooled), then the retained set.
+    Only a forward that holds the whole prompt (its queries are every cached
+    token) freezes a set; otherwise the layer keeps none and decodes over
+    every block."""
+    _FROZEN.pop(id(module), None)
+    L, _ = _prompt_len(key, attention_mask)
+    if L is None or L != query.shape[2]:
+        return
+    Q, K = query[0], key[0, :, :L]
+    if sel == "h2o":
+        imp = _brt.h2o_key_importance_torch(Q, K)
+    else:
+        imp = _brt.snapkv_key_importance_torch(Q, K, obs_window=int(cfg["obs_window"]),
+                                               pool_kernel=int(cfg["pool_kernel"]))
+    bs = int(cfg["block_size"])
+    mask, table, lens = _brt.retain_blocks_table(imp, bs, L, int(cfg["avg_budget"]), cfg["n_sink_blocks"],
+                                                 cfg["n_local_blocks"], cfg["c_min"])
+    _FROZEN[id(module)] = _Frozen(mask, table, lens, ops.n_blocks(L, bs))
+
+
+def _frozen_decode(module, query, key, value, attention_mask, scaling, cfg):
+    """One decode step over the frozen set plus the current sink and local
+    blocks (patch.py:76-87, 114-121); None when the mask is not a prefix run."""
+    L, lens_dev = _prompt_len(key, attention_mask)
+    if L is None:
+        return None
+    bs = int(cfg["block_size"])
+    nb_now = ops.n_blocks(L, bs)
+    Hq = query.shape[1]
+    fr = _FROZEN.get(id(module))
+    if fr is not None and fr.nbp <= nb_now:
+        table, lens = _brt.frozen_table(fr.table, fr.lens, fr.nbp, nb_now, int(cfg["n_sink_blocks"]),
+                                        int(cfg["n_local_blocks"]))
+    else:                                        # prefill not seen: every block (patch.py:80-81)
+        key_ = (query.device, Hq)
+        empty = _ALL_BLOCKS.get(key_)
+        if empty is None:
+            empty = (torch.zeros(Hq, 1, dtype=torch.int32, device=query.device),
+                     torch.zeros(Hq, dtype=torch.int32, device=query.device))
+            _ALL_BLOCKS[key_] = empty
+        table, lens = _brt.frozen_table(empty[0], empty[1], 0, nb_now, nb_now, 0)
+    if instrumentation_active():
+        record_selection(table, lens, nb_now)
+    out = torch.empty(1, 1, Hq, query.shape[3], dtype=query.dtype, device=query.device)
+    ops.sparse_decode(query[:, :, 0, :], key, value, table[None], lens[None], bs, sm_scale=scaling,
+                      seq_lens=lens_dev, out=out[:, 0])
+    return out
+
+
 @torch.compiler.disable
 def adakv_attention_forward(module, query, key, value, attention_mask, scaling, dropout=0.0,
                             **kwargs):
@@ -152,14 +240,23 @@ def adakv_attention_forward(module, query, key, value, attention_mask, scaling, 
     """
     cfg = _ADAKV_CFG
     B, Hq, q_len, D = query.shape
+    sel = cfg.get("selection", "adakv")
+    if sel not in ("adakv", "h2o", "snapkv"):
+        raise ValueError(f"unknown selection: {sel!r}")
+    if sel != "adakv":
+        if cfg["enabled"] and B == 1 and q_len > 1:
+            _capture_frozen(module, query, key, attention_mask, cfg, sel)   # the output stays dense
+        elif cfg["enabled"] and B == 1:
+            out = _frozen_decode(module, query, key, value, attention_mask, scaling, cfg)
+            if out is not None:
+                return out, None
+        return _SDPA(module, query, key, value, attention_mask=attention_mask, scaling=scaling,
+                     dropout=dropout, **kwargs)
     if (not cfg["enabled"]) or q_len != 1:
         if q_len != 1:
             _STATE.pop(id(module), None)        # a new prefill starts a new sequence
         return _SDPA(module, query, key, value, attention_mask=attention_mask, scaling=scaling,
                      dropout=dropout, **kwargs)
-    if cfg.get("selection", "adakv") != "adakv":
-        raise NotImplementedError(
-            f"selection={cfg['selection']!r} (eviction baselines) is not part of the HIP path")
     if cfg["estimator"] not in ("centroid", "minmax"):
         raise ValueError(f"unknown estimator: {cfg['estimator']!r}")
     bs = int(cfg["block_size"])
@@ -223,6 +320,7 @@ def enable_adakv(**cfg):
     _ADAKV_CFG.update(cfg)
     _ADAKV_CFG["enabled"] = True
     _STATE.clear()
+    _FROZEN.clear()                              # frozen sets of a previous configuration
 
 
 def disable_adakv():

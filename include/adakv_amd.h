@@ -36,6 +36,14 @@
  *   adakv_decode_fused     <- adakv_decode_attention             adakv/attention.py:250-268
  *                             adakv_decode_step                  adakv/runtime.py:85-112
  *   adakv_dense_decode     <- dense_decode                       benchmarks/efficiency/bench_decode_latency.py:40-53
+ * Eviction baselines (a retained set frozen at prefill, adakv/baselines_rt.py):
+ *   adakv_key_importance   <- h2o_key_importance_torch           adakv/baselines_rt.py:43-64
+ *                             snapkv_key_importance_torch (window) adakv/baselines_rt.py:67-78
+ *   adakv_importance_pool  <- the max_pool1d of snapkv_key_importance_torch  adakv/baselines_rt.py:79-80
+ *   adakv_retain_blocks    <- retain_blocks_torch                adakv/baselines_rt.py:83-127
+ *   adakv_frozen_table     <- frozen_decode_block_table          adakv/baselines_rt.py:158-205
+ *   adakv_mask_table       <- mask_to_block_table                adakv/baselines_rt.py:139-155
+ *                             (and frozen_decode_block_table on a mask)
  */
 #ifndef ADAKV_AMD_H
 #define ADAKV_AMD_H
@@ -47,7 +55,7 @@
 extern "C" {
 #endif
 
-#define ADAKV_ABI_VERSION 3
+#define ADAKV_ABI_VERSION 4
 
 /* Status codes.  Argument errors are detected on the host before any launch. */
 enum {
@@ -188,6 +196,70 @@ int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const 
 int adakv_dense_decode(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
                        const int32_t* seq_lens, float sm_scale, const adakv_output_t* out,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- Eviction baselines (H2O, SnapKV) ----------------------------------------
+ * A retained block set is chosen once from the prompt's own attention and
+ * frozen; decode steps attend it plus the current sink and local blocks
+ * through adakv_sparse_decode.  Prompt of ONE sequence:
+ *   q [n_q_heads, n_tokens, head_dim], k [n_kv_heads, n_tokens, head_dim]
+ * (q-head h reads KV head h / (n_q_heads / n_kv_heads)); tables are
+ * adakv_selection_t rows [n_heads, table_width] (batch 1). */
+typedef struct {
+  const void* q;
+  const void* k;
+  int32_t dtype;                 /* shared by q and k                                   */
+  int32_t n_q_heads, n_kv_heads;
+  int32_t head_dim;              /* 64 or 128                                           */
+  int32_t n_tokens;              /* 1 .. 1048576                                        */
+  int64_t q_stride_h, q_stride_s;  /* elements; 16-byte aligned rows                    */
+  int64_t k_stride_h, k_stride_s;
+} adakv_prompt_t;
+
+/* Workspace of adakv_key_importance: one fp32 per (q-head, query >= first_query). */
+size_t adakv_importance_workspace_bytes(const adakv_prompt_t* p, int32_t first_query);
+
+/* importance[h, j] = sum over the queries i in [first_query, n_tokens) with
+ * i >= j of softmax_j(q_i . k_j * sm_scale), fp32 [n_q_heads, pitch],
+ * pitch >= n_tokens.  first_query 0 is H2O's accumulated attention;
+ * n_tokens - obs_window is SnapKV's observation window before its pool
+ * (adakv/baselines.py:63-79, 95-115).  Matrix-core dot products with fp32
+ * accumulation; deterministic. */
+int adakv_key_importance(const adakv_prompt_t* p, int32_t first_query, float sm_scale, float* importance,
+                         int32_t pitch, void* workspace, size_t workspace_bytes, void* stream);
+
+/* out[h, t] = max of in[h, u] over |u - t| <= kernel / 2 clipped to
+ * [0, n_tokens) (odd kernel; in and out must not overlap).  adakv/baselines.py:82-92. */
+int adakv_importance_pool(const float* in, float* out, int32_t n_heads, int32_t n_tokens, int32_t pitch,
+                          int32_t kernel, void* stream);
+
+/* The frozen retained set of each head: k = min(max(budget, floor), nb)
+ * blocks (nb = ceil(n_real / block_size), floor = min(sink + local + c_min, nb)),
+ * the sink and local blocks plus the content blocks of largest importance sum
+ * over their real tokens (fp64 sums compared in fp32; ties: lower block first).
+ * mask uint8 [n_heads, mask_pitch] gets 1/0 for blocks [0, nb); when sel is not
+ * NULL it also receives the retained blocks ascending (table_width >= k,
+ * sel_lens = k).  nb <= 16384.  adakv/baselines.py:120-160. */
+int adakv_retain_blocks(const float* importance, int32_t n_heads, int32_t pitch, int32_t n_real,
+                        int32_t block_size, int32_t budget, int32_t n_sink_blocks, int32_t n_local_blocks,
+                        int32_t c_min, uint8_t* mask, int32_t mask_pitch, const adakv_selection_t* sel,
+                        void* stream);
+
+/* Decode-step table of a frozen set: per head, the frozen blocks (frozen
+ * rows, sel_lens entries each, ids < n_frozen_blocks) united with the sink and
+ * local blocks of nb_now >= n_frozen_blocks blocks, ascending, count in
+ * out->sel_lens.  out->table_width >= min(nb_now, frozen width + sink + local);
+ * nb_now <= 65536. */
+int adakv_frozen_table(const adakv_selection_t* frozen, int32_t n_heads, int32_t n_frozen_blocks, int32_t nb_now,
+                       int32_t n_sink_blocks, int32_t n_local_blocks, const adakv_selection_t* out,
+                       void* stream);
+
+/* Ascending table of the nonzero entries of each mask row [0, n_mask_blocks)
+ * united with the sink and local blocks of nb_now >= n_mask_blocks blocks
+ * (n_sink_blocks = n_local_blocks = 0, nb_now = n_mask_blocks: the mask
+ * alone); table_width >= nb_now, count in sel_lens; nb_now <= 65536. */
+int adakv_mask_table(const uint8_t* mask, int32_t n_heads, int32_t mask_pitch, int32_t n_mask_blocks,
+                     int32_t nb_now, int32_t n_sink_blocks, int32_t n_local_blocks, const adakv_selection_t* out,
+                     void* stream);
 
 #ifdef __cplusplus
 }

@@ -36,6 +36,9 @@ __all__ = [
     "budget_weights", "budget_bounds", "allocate_budget", "select_blocks",
     "sparse_attention", "plan_table", "ref_from_table", "centroid_after_append",
     "selection_near_ties", "budget_near_half", "budget_extra",
+    "key_importance", "h2o_key_importance", "maxpool_same", "snapkv_key_importance",
+    "retain_block_sums", "retain_blocks", "retain_near_ties", "frozen_decode_mask",
+    "frozen_sparse_attention",
 ]
 
 
@@ -309,3 +312,146 @@ def budget_near_half(w: np.ndarray, lo: int, target: float, margin: float = 1e-3
     boundary (budget.py:85), where a last-ulp change of the weights flips k."""
     x = lo + budget_extra(np.asarray(w, dtype=np.float64), lo, target)
     return np.abs((x - np.floor(x)) - 0.5) <= margin
+
+
+# --------------------------------------------------------------------------
+# Eviction baselines (H2O, SnapKV): a retained block set frozen at prefill
+# from the prompt's own attention (adakv/baselines.py, adakv/baselines_rt.py).
+# Q, K are [H, S, D] expanded to query heads, as in the reference.
+# --------------------------------------------------------------------------
+def key_importance(Q: np.ndarray, K: np.ndarray, first_query: int = 0) -> np.ndarray:
+    """Attention each key receives, summed over the causal queries at
+    positions [first_query, S): fp64 logits q_i . k_j / sqrt(D) for j <= i,
+    row softmax over keys, column sums, fp32 result [H, S].
+
+    first_query = 0 is H2O's accumulated attention (baselines.py:63-79);
+    first_query = S - min(obs_window, S) is SnapKV's window before its pool
+    (baselines.py:101-114).  Rows are processed in slices so that only
+    [H, rows, S] is live at once."""
+    H, S, D = K.shape
+    if Q.shape != (H, S, D):
+        raise AssertionError("Q and K must share [H, S, D]")
+    first_query = int(min(max(first_query, 0), S))
+    Kd = K.astype(np.float64)
+    inv = 1.0 / np.sqrt(D)
+    imp = np.zeros((H, S), dtype=np.float64)
+    keys = np.arange(S)
+    step = 256
+    for i0 in range(first_query, S, step):
+        i1 = min(i0 + step, S)
+        logits = np.einsum("hid,hjd->hij", Q[:, i0:i1].astype(np.float64), Kd) * inv
+        visible = keys[None, :] <= np.arange(i0, i1)[:, None]           # key j <= query i
+        logits = np.where(visible[None], logits, -np.inf)
+        imp += _softmax_rows(logits).sum(axis=1)
+    return imp.astype(np.float32)
+
+
+def h2o_key_importance(Q: np.ndarray, K: np.ndarray) -> np.ndarray:
+    """H2O heavy-hitter signal: every prompt query (baselines.py:63-79)."""
+    return key_importance(Q, K, 0)
+
+
+def maxpool_same(x: np.ndarray, kernel: int) -> np.ndarray:
+    """Same-length max over the window [t - kernel//2, t + kernel//2] of the
+    last axis, clipped to the array (edge padding, baselines.py:82-92; for a
+    max, equal to torch's -inf padding, baselines_rt.py:79-80)."""
+    if kernel <= 1:
+        return x
+    r = kernel // 2
+    S = x.shape[-1]
+    out = np.empty_like(x)
+    for t in range(S):
+        out[..., t] = x[..., max(0, t - r):min(S, t + r + 1)].max(axis=-1)
+    return out
+
+
+def snapkv_key_importance(Q: np.ndarray, K: np.ndarray, obs_window: int = 32,
+                          pool_kernel: int = 7) -> np.ndarray:
+    """SnapKV: attention from the last obs_window queries, max-pooled over
+    key positions (baselines.py:95-115)."""
+    S = K.shape[1]
+    w = int(min(obs_window, S))
+    return maxpool_same(key_importance(Q, K, S - w), pool_kernel).astype(np.float32)
+
+
+def retain_block_sums(importance: np.ndarray, block_size: int, n_real: int) -> np.ndarray:
+    """fp64 sum of each block's importance over its real tokens (baselines.py:139-143)."""
+    H = importance.shape[0]
+    nb = -(-n_real // block_size)
+    blk = np.zeros((H, nb), dtype=np.float64)
+    for b in range(nb):
+        s, e = b * block_size, min((b + 1) * block_size, n_real)
+        blk[:, b] = importance[:, s:e].astype(np.float64).sum(axis=1)
+    return blk
+
+
+def retain_blocks(importance: np.ndarray, block_size: int, n_real: int, budget: int,
+                  n_sink_blocks: int = 1, n_local_blocks: int = 4, c_min: int = 1) -> np.ndarray:
+    """Frozen retained mask [H, nb]: k = min(max(budget, floor), nb) blocks
+    per head -- the sink and local blocks, then the content blocks of largest
+    block sum (baselines.py:120-160).  Equal sums are taken in ascending block
+    order (a stable descending sort); the reference's unstable argsort leaves
+    that order unspecified, so tests exclude near-ties."""
+    blk = retain_block_sums(importance, block_size, n_real)
+    H, nb = blk.shape
+    sink, local = min(n_sink_blocks, nb), min(n_local_blocks, nb)
+    biased = blk.copy()
+    biased[:, :sink] = np.inf
+    if local:
+        biased[:, nb - local:] = np.inf
+    floor = min(sink + local + c_min, nb)
+    k = min(max(int(budget), floor), nb)
+    mask = np.zeros((H, nb), dtype=bool)
+    for h in range(H):
+        mask[h, np.argsort(-biased[h], kind="stable")[:k]] = True
+        mask[h, :sink] = True
+        if local:
+            mask[h, nb - local:] = True
+    return mask
+
+
+def retain_near_ties(importance: np.ndarray, block_size: int, n_real: int, budget: int,
+                     n_sink_blocks: int, n_local_blocks: int, c_min: int,
+                     rel_tol: float = 1e-5) -> np.ndarray:
+    """Per-head flag: the last retained and first evicted content block sums
+    are within rel_tol * (largest block sum of the head)."""
+    blk = retain_block_sums(importance, block_size, n_real)
+    H, nb = blk.shape
+    sink, local = min(n_sink_blocks, nb), min(n_local_blocks, nb)
+    content = np.arange(sink, max(nb - local, sink))
+    k = min(max(int(budget), min(sink + local + c_min, nb)), nb)
+    take = k - (sink + len(set(range(nb - local, nb)) - set(range(sink))))
+    flags = np.zeros((H,), dtype=bool)
+    if content.size == 0 or take <= 0 or take >= content.size:
+        return flags
+    for h in range(H):
+        s = np.sort(blk[h, content])[::-1]
+        flags[h] = (s[take - 1] - s[take]) <= rel_tol * max(float(blk[h].max()), 1e-30)
+    return flags
+
+
+def frozen_decode_mask(fmask: np.ndarray, nb_now: int, n_sink_blocks: int,
+                       n_local_blocks: int) -> np.ndarray:
+    """Decode-time retained set [H, nb_now]: the frozen prefill set plus the
+    sink and the local window of the current blocks (baselines_rt.py:182-205)."""
+    H, nbp = fmask.shape
+    if nb_now < nbp:
+        raise AssertionError("decode block count must not shrink below prefill")
+    sink, local = min(n_sink_blocks, nb_now), min(n_local_blocks, nb_now)
+    m = np.zeros((H, nb_now), dtype=bool)
+    m[:, :nbp] = fmask
+    m[:, :sink] = True
+    if local:
+        m[:, nb_now - local:] = True
+    return m
+
+
+def frozen_sparse_attention(q: np.ndarray, K: np.ndarray, V: np.ndarray, retained_mask: np.ndarray,
+                            block_size: int):
+    """One decode step over the retained blocks only (baselines.py:197-212):
+    (out [H, D], counts [H])."""
+    H, S, D = K.shape
+    tok = np.repeat(retained_mask, block_size, axis=1)[:, :S]
+    logits = np.einsum("hd,hsd->hs", q, K) / np.sqrt(D)
+    out = np.einsum("hs,hsd->hd", _softmax_rows(np.where(tok, logits, -np.inf)), V)
+    return out, retained_mask.sum(axis=1)

@@ -15,6 +15,8 @@ random-init Llama routed through ``patch_model``.
   first real token; with every block selected it equals SDPA over the mask.
 * A mask row that is not one contiguous run goes to SDPA.
 * A normal budget: the realised mean budget is the requested one.
+* The eviction baselines (selection "h2o" / "snapkv"): a full budget equals
+  SDPA, a normal budget keeps the frozen count, batches go to SDPA.
 """
 from __future__ import annotations
 
@@ -197,4 +199,42 @@ def test_generate_with_static_cache_matches_sdpa_greedy():
     A.stop_budget_trace()
     disable_adakv()
     assert len(trace) == (new - 1) * 2, f"{len(trace)} layer-steps on the HIP path"
+    assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("sel", ["h2o", "snapkv"])
+@pytest.mark.parametrize("cache_kind", ["dynamic", "static"])
+def test_eviction_full_budget_equals_sdpa(sel, cache_kind):
+    """selection="h2o"/"snapkv" (adakv/patch.py:57-87): a budget that retains
+    every block freezes the whole prompt, so decoding over the frozen set plus
+    the new tail equals SDPA; every decode step ran on the HIP path."""
+    say(f"patch {sel} fp32 full budget, {cache_kind} cache")
+    model = _model(torch.float32)
+    got, ref, trace = _run(model, _ids(1), cache_kind, _cfg(selection=sel, **FULL))
+    assert len(trace) == STEPS * 2, "the frozen decode did not run on every layer of every step"
+    err = (got - ref).abs().max().item()
+    say(f"  max |logit diff| {err:.2e}")
+    assert err <= 2e-3 * max(ref.abs().max().item(), 1.0)
+
+
+@pytest.mark.parametrize("sel", ["h2o", "snapkv"])
+def test_eviction_normal_budget_keeps_the_frozen_count(sel):
+    """avg_budget 8: every head keeps 8 frozen blocks of the 19-block prompt;
+    the decode tokens stay inside the last block, so each step attends 8."""
+    say(f"patch {sel} bf16 avg_budget 8")
+    model = _model(torch.bfloat16)
+    got, ref, trace = _run(model, _ids(1), "dynamic", _cfg(selection=sel, avg_budget=8))
+    assert trace == [8.0] * (STEPS * 2), trace
+    assert torch.isfinite(got).all()
+    rel = ((got - ref).norm() / ref.norm()).item()
+    say(f"  logits rel L2 vs dense {rel:.2e}")
+
+
+def test_eviction_batches_go_to_sdpa():
+    """As in the reference (patch.py:96-100), the eviction baselines decode
+    single sequences only; a batch of two is SDPA's."""
+    say("patch h2o, batch of 2 -> SDPA")
+    model = _model(torch.bfloat16)
+    got, ref, trace = _run(model, _ids(2), "dynamic", _cfg(selection="h2o"))
+    assert len(trace) == 0
     assert torch.equal(got, ref)
