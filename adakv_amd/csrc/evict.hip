@@ -59,7 +59,25 @@ struct ImpArgs {
   float* lse;                  // [Hq, L - q0], base-2 log-sum-exp
   float* imp;                  // [Hq, pitch]
   int pitch;
+  int nsplit, klen;            // pass 1 key split: nsplit ranges of klen keys (a multiple of 16)
+  float2* part;                // nsplit > 1: partial (max, sum) [Hq, nsplit, L - q0]
 };
+
+// Workgroup x index -> q-head.  Consecutive workgroups go to the 8 XCDs in
+// turn, each with its own L2; with Hq % 8 == 0 this puts the q-heads
+// [x*Hq/8, (x+1)*Hq/8) on XCD x, so the q-heads of a KV group (adjacent heads)
+// share their keys through one L2.
+__device__ __forceinline__ int head_of(int bx, int Hq) {
+  return (Hq % 8 == 0) ? (bx % 8) * (Hq / 8) + bx / 8 : bx;
+}
+
+__device__ __forceinline__ void softmax_merge(float& m, float& l, float m2, float l2) {
+  const float mx = fmaxf(m, m2);
+  if (mx == -INFINITY) return;
+  l = (m == -INFINITY ? 0.f : l * __builtin_amdgcn_exp2f(m - mx)) +
+      (m2 == -INFINITY ? 0.f : l2 * __builtin_amdgcn_exp2f(m2 - mx));
+  m = mx;
+}
 
 // One lane's slice of a 16-row tile: lane (col, grp) holds row col, elements
 // [STEP*s + SUB*grp, +SUB) of k-step s -- the A/B operand layout of the 16x16
@@ -103,17 +121,20 @@ __device__ __forceinline__ float4_t tile_dot(const Frag<DT, D>& a, const Frag<DT
 
 // ---- pass 1: log-sum-exp of every query row --------------------------------
 // Wave: queries [q0 + qw, +64) resident as B (columns), keys streamed as A
-// rows 16 at a time over [0, last query].  Lane (col, grp) keeps an online
-// (max, sum) for query col of each resident tile over keys 4*grp + i of each
-// step; the four lanes of a column merge at the end.
+// rows 16 at a time over [0, last query] -- or, when the queries are too few
+// to fill the GPU (SnapKV's window), over one of nsplit key ranges, whose
+// partial (max, sum) importance_merge_kernel combines.  Lane (col, grp) keeps
+// an online (max, sum) for query col of each resident tile over keys
+// 4*grp + i of each step; the four lanes of a column merge at the end.
 template <int DT, int D>
 __global__ __launch_bounds__(kEvNT) void importance_lse_kernel(ImpArgs a) {
-  const int h = blockIdx.x;
+  const int h = head_of(blockIdx.x, a.Hq);
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const int col = lane & 15, grp = lane >> 4;
   const int nq = a.L - a.q0;
+  const int split = blockIdx.y % a.nsplit, nqc = gridDim.y / a.nsplit;
   // the last queries see the most keys: dispatched first
-  const int qw = ((gridDim.y - 1 - blockIdx.y) * (kEvNT / kWave) + w) * kEvRows;
+  const int qw = ((nqc - 1 - (int)blockIdx.y / a.nsplit) * (kEvNT / kWave) + w) * kEvRows;
   if (qw >= nq) return;                                   // uniform over the wave; no barriers below
   const char* qb = a.q + (int64_t)h * a.qsh;
   const char* kb = a.k + (int64_t)(h / a.G) * a.ksh;
@@ -121,10 +142,11 @@ __global__ __launch_bounds__(kEvNT) void importance_lse_kernel(ImpArgs a) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) qf[t].load(qb + (int64_t)min(a.q0 + qw + 16 * t + col, a.L - 1) * a.qss, grp);
   const int qlast = min(a.q0 + qw + kEvRows, a.L) - 1;
+  const int jb = split * a.klen, je = min(jb + a.klen, qlast + 1);
   float m[4], l[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) { m[t] = -INFINITY; l[t] = 0.f; }
-  for (int j0 = 0; j0 <= qlast; j0 += 16) {
+  for (int j0 = jb; j0 < je; j0 += 16) {
     Frag<DT, D> kf;
     kf.load(kb + (int64_t)min(j0 + col, a.L - 1) * a.kss, grp);
 #pragma unroll
@@ -149,18 +171,26 @@ __global__ __launch_bounds__(kEvNT) void importance_lse_kernel(ImpArgs a) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
 #pragma unroll
-    for (int o = 16; o <= 32; o <<= 1) {
-      const float m2 = __shfl_xor(m[t], o), l2 = __shfl_xor(l[t], o);
-      const float mx = fmaxf(m[t], m2);
-      if (mx != -INFINITY) {
-        l[t] = (m[t] == -INFINITY ? 0.f : l[t] * __builtin_amdgcn_exp2f(m[t] - mx)) +
-               (m2 == -INFINITY ? 0.f : l2 * __builtin_amdgcn_exp2f(m2 - mx));
-        m[t] = mx;
-      }
-    }
+    for (int o = 16; o <= 32; o <<= 1) softmax_merge(m[t], l[t], __shfl_xor(m[t], o), __shfl_xor(l[t], o));
     const int qo = qw + 16 * t + col;
-    if (grp == 0 && qo < nq) a.lse[(int64_t)h * nq + qo] = m[t] + log2f(l[t]);
+    if (grp == 0 && qo < nq) {
+      if (a.nsplit == 1) a.lse[(int64_t)h * nq + qo] = m[t] + log2f(l[t]);
+      else a.part[((int64_t)h * a.nsplit + split) * nq + qo] = make_float2(m[t], l[t]);
+    }
   }
+}
+
+// Pass 1 with a key split: lse of each (q-head, query) from its partials.
+__global__ __launch_bounds__(256) void importance_merge_kernel(ImpArgs a) {
+  const int nq = a.L - a.q0;
+  const int qo = blockIdx.x * 256 + threadIdx.x, h = blockIdx.y;
+  if (qo >= nq) return;
+  float m = -INFINITY, l = 0.f;
+  for (int s = 0; s < a.nsplit; ++s) {
+    const float2 p = a.part[((int64_t)h * a.nsplit + s) * nq + qo];
+    softmax_merge(m, l, p.x, p.y);
+  }
+  a.lse[(int64_t)h * nq + qo] = m + log2f(l);
 }
 
 // ---- pass 2: column sums ------------------------------------------------------
@@ -170,7 +200,7 @@ __global__ __launch_bounds__(kEvNT) void importance_lse_kernel(ImpArgs a) {
 // summed at the end.
 template <int DT, int D>
 __global__ __launch_bounds__(kEvNT) void importance_colsum_kernel(ImpArgs a) {
-  const int h = blockIdx.x;
+  const int h = head_of(blockIdx.x, a.Hq);
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const int col = lane & 15, grp = lane >> 4;
   const int nq = a.L - a.q0;
@@ -357,18 +387,38 @@ __global__ __launch_bounds__(kUnionNT) void union_table_kernel(UnionArgs a) {
   table_from_bits<kUnionNT>(bits, a.n, a.table + (int64_t)h * a.width, a.width, a.lens + h, scan);
 }
 
+// Pass-1 key splits: one per query-chunk wave while those waves fill the GPU
+// (H2O); otherwise (few queries: SnapKV's window) enough splits for about
+// 2048 waves, each over at least 1024 keys.
+int lse_splits(int Hq, int nq, int L) {
+  const int64_t waves = (int64_t)Hq * ((nq + kEvRows - 1) / kEvRows);
+  if (waves >= 1024) return 1;
+  return (int)std::max<int64_t>(1, std::min<int64_t>((2048 + waves - 1) / waves, (L + 1023) / 1024));
+}
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+size_t importance_ws(int Hq, int nq, int L) {
+  const int ns = lse_splits(Hq, nq, L);
+  const size_t lse = align256((size_t)Hq * nq * sizeof(float));
+  return ns == 1 ? lse : lse + (size_t)Hq * ns * nq * sizeof(float2);
+}
+
 template <int DT>
-hipError_t launch_importance_dt(const ImpArgs& a, int D, hipStream_t s) {
+hipError_t launch_importance_dt(ImpArgs a, int D, hipStream_t s) {
+  constexpr int kRowsPerGroup = kEvNT / kWave * kEvRows;
   const int nq = a.L - a.q0;
-  const dim3 g1(a.Hq, (nq + kEvNT / kWave * kEvRows - 1) / (kEvNT / kWave * kEvRows));
-  const dim3 g2(a.Hq, (a.L + kEvNT / kWave * kEvRows - 1) / (kEvNT / kWave * kEvRows));
-  if (D == 64) {
-    importance_lse_kernel<DT, 64><<<g1, kEvNT, 0, s>>>(a);
-    importance_colsum_kernel<DT, 64><<<g2, kEvNT, 0, s>>>(a);
-  } else {
-    importance_lse_kernel<DT, 128><<<g1, kEvNT, 0, s>>>(a);
-    importance_colsum_kernel<DT, 128><<<g2, kEvNT, 0, s>>>(a);
-  }
+  a.nsplit = lse_splits(a.Hq, nq, a.L);
+  a.klen = (a.L + a.nsplit - 1) / a.nsplit;
+  a.klen = (a.klen + 15) / 16 * 16;
+  a.part = reinterpret_cast<float2*>(reinterpret_cast<char*>(a.lse) + align256((size_t)a.Hq * nq * sizeof(float)));
+  const dim3 g1(a.Hq, ((nq + kRowsPerGroup - 1) / kRowsPerGroup) * a.nsplit);
+  const dim3 g2(a.Hq, (a.L + kRowsPerGroup - 1) / kRowsPerGroup);
+  if (D == 64) importance_lse_kernel<DT, 64><<<g1, kEvNT, 0, s>>>(a);
+  else importance_lse_kernel<DT, 128><<<g1, kEvNT, 0, s>>>(a);
+  if (a.nsplit > 1) importance_merge_kernel<<<dim3((nq + 255) / 256, a.Hq), 256, 0, s>>>(a);
+  if (D == 64) importance_colsum_kernel<DT, 64><<<g2, kEvNT, 0, s>>>(a);
+  else importance_colsum_kernel<DT, 128><<<g2, kEvNT, 0, s>>>(a);
   return hipGetLastError();
 }
 
@@ -405,7 +455,7 @@ extern "C" {
 
 size_t adakv_importance_workspace_bytes(const adakv_prompt_t* p, int32_t first_query) {
   if (check_prompt(p) != ADAKV_OK || first_query < 0 || first_query >= p->n_tokens) return 0;
-  return (size_t)p->n_q_heads * (size_t)(p->n_tokens - first_query) * sizeof(float);
+  return importance_ws(p->n_q_heads, p->n_tokens - first_query, p->n_tokens);
 }
 
 int adakv_key_importance(const adakv_prompt_t* p, int32_t first_query, float sm_scale, float* importance,
@@ -415,7 +465,8 @@ int adakv_key_importance(const adakv_prompt_t* p, int32_t first_query, float sm_
   if (!importance || !ws) return ADAKV_ERR_NULL;
   if (first_query < 0 || first_query >= p->n_tokens || !isfinite(sm_scale)) return ADAKV_ERR_VALUE;
   if (pitch < p->n_tokens) return ADAKV_ERR_SHAPE;
-  if (ws_bytes < adakv_importance_workspace_bytes(p, first_query) || !aligned16(ws)) return ADAKV_ERR_WORKSPACE;
+  if (ws_bytes < adakv_importance_workspace_bytes(p, first_query) || ((uintptr_t)ws & 255u))
+    return ADAKV_ERR_WORKSPACE;
   const int el = p->dtype == ADAKV_F32 ? 4 : 2;
   ImpArgs a;
   a.q = reinterpret_cast<const char*>(p->q);
@@ -427,6 +478,7 @@ int adakv_key_importance(const adakv_prompt_t* p, int32_t first_query, float sm_
   a.c2 = (float)((double)sm_scale * 1.4426950408889634);
   a.lse = reinterpret_cast<float*>(ws);
   a.imp = importance; a.pitch = pitch;
+  a.nsplit = 1; a.klen = p->n_tokens; a.part = nullptr;   // set by the launcher
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   switch (p->dtype) {

@@ -24,7 +24,10 @@ bench_decode_latency.py:11-19) on the same layers at the same avg_budget:
 quest (minmax bounds + fixed budget), adakv_cf (centroids + fixed budget),
 adakv_nucleus (centroids + the nucleus budget, the cell that table labels
 "adakv"), streaming (sink + most recent blocks, no scoring) and dense, with
-each estimator's summary bytes per layer.
+each estimator's summary bytes per layer.  ``eviction`` holds the H2O /
+SnapKV baselines (adakv/baselines_rt.py): the prefill-side key importance
+against its roofline and the reference's torch formulation, the retention,
+and the frozen decode step on the same layers.
 """
 from __future__ import annotations
 
@@ -36,6 +39,7 @@ import sys
 import time
 
 PEAK_HBM_GBPS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0          # dense bf16 matrix-core peak
 METRIC = "decode attn µs/layer @128K + achieved HBM GB/s (KV bytes touched), 1 MI355X"
 
 
@@ -58,6 +62,8 @@ def parse():
     ap.add_argument("--no-sweep", action="store_true", help="skip the context sweep")
     ap.add_argument("--no-ragged", action="store_true", help="skip the ragged-batch leg (BASELINE config 4)")
     ap.add_argument("--sweep-ctx", type=str, default="4096,16384,32768,65536,262144")
+    ap.add_argument("--no-evict", action="store_true", help="skip the H2O / SnapKV eviction-baseline legs")
+    ap.add_argument("--h2o-len", type=int, default=8192, help="prompt length of the H2O importance leg")
     ap.add_argument("--model-step", action="store_true",
                     help="BASELINE config 5 instead: a Llama-3-70B-shaped 80-layer decode step through patch_model")
     ap.add_argument("--model-layers", type=int, default=80)
@@ -299,6 +305,106 @@ def cpu_baseline(torch, w: Workload, budget_s: float):
     return float(np.median(runs)), len(times)
 
 
+def time_calls(torch, fn, n, warm=1):
+    """HIP-event time per call of fn() on the current stream (ms)."""
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(n):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / n
+
+
+def torch_key_importance(torch, Q, K, first, chunk=256):
+    """The reference runtime's formulation (adakv/baselines_rt.py:43-80): fp32
+    logits per chunk of queries against every key, causal mask, softmax over
+    keys, summed over the chunk -- torch ops on the same GPU, for comparison."""
+    Hq, L, D = Q.shape
+    G = Hq // K.shape[0]
+    Kt = K.float().repeat_interleave(G, dim=0).transpose(1, 2).contiguous()      # [Hq, D, L]
+    imp = torch.zeros(Hq, L, device=Q.device)
+    keys = torch.arange(L, device=Q.device)
+    for s0 in range(first, L, chunk):
+        e0 = min(s0 + chunk, L)
+        lg = torch.bmm(Q[:, s0:e0].float(), Kt) / math.sqrt(D)
+        lg = lg.masked_fill(keys.view(1, 1, -1) > torch.arange(s0, e0, device=Q.device).view(1, -1, 1),
+                            float("-inf"))
+        imp += torch.softmax(lg, dim=-1).sum(dim=1)
+    return imp
+
+
+def evict_bench(torch, ops, w, stream, seed, h2o_len):
+    """The eviction baselines (adakv/baselines_rt.py): the prefill-side
+    importance (H2O over an h2o_len prompt, SnapKV's 32-query window over the
+    headline 128K context) against the matrix-core and HBM rooflines and
+    against the reference's torch formulation, the retention, and the frozen
+    decode step on the headline workload."""
+    from adakv_amd import baselines_rt as BR
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    res = {}
+    L = h2o_len
+    Q = torch.randn(w.Hq, L, w.D, device=dev, dtype=torch.bfloat16, generator=gen)
+    K = torch.randn(w.Hkv, L, w.D, device=dev, dtype=torch.bfloat16, generator=gen)
+    ms = time_calls(torch, lambda: BR.key_importance(Q, K, 0), 5)
+    ms_t = time_calls(torch, lambda: torch_key_importance(torch, Q, K, 0), 2)
+    flops = 2 * w.Hq * (L * (L + 1) // 2) * 2 * w.D        # two passes over the causal (query, key) pairs
+    tf = flops / (ms * 1e-3) / 1e12
+    res["h2o_importance"] = {"prompt": L, "ms": round(ms, 3), "TFLOPs": round(tf, 1),
+                             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
+                                          "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4)},
+                             "torch_formulation_ms": round(ms_t, 2), "speedup_vs_torch": round(ms_t / ms, 1)}
+    log(f"h2o importance, {L}-token prompt: {ms:.3f} ms ({tf:.0f} TFLOP/s useful); torch formulation {ms_t:.1f} ms")
+    del Q, K
+    S = w.S
+    Qs = torch.randn(w.Hq, S, w.D, device=dev, dtype=torch.bfloat16, generator=gen)
+    Ks = w.k[0][0]
+    win = 32
+    g_snap = capture(torch, lambda l: BR.snapkv_key_importance_torch(Qs, Ks, win, 7), 1, stream)
+    ms_s, _ = time_graph(torch, g_snap, 20, 2)
+    ms_s /= 20
+    ms_st = time_calls(torch, lambda: torch_key_importance(torch, Qs, Ks, S - win), 3)
+    sbytes = w.Hkv * S * w.D * 2 + w.Hq * win * w.D * 2 + w.Hq * S * 4 * 2   # K, window, importance (+pool)
+    sg = sbytes / (ms_s * 1e-3) / 1e9
+    res["snapkv_importance"] = {"prompt": S, "window": win, "pool": 7, "us": round(ms_s * 1e3, 1),
+                                "GBps": round(sg, 1),
+                                "roofline": {"bound": "hbm", "achieved": round(sg, 1), "peak": PEAK_HBM_GBPS,
+                                             "unit": "GB/s", "frac": round(sg / PEAK_HBM_GBPS, 4),
+                                             "bytes": int(sbytes)},
+                                "torch_formulation_us": round(ms_st * 1e3, 1),
+                                "speedup_vs_torch": round(ms_st / ms_s, 1)}
+    log(f"snapkv importance, {S}-token prompt: {ms_s * 1e3:.1f} us ({sg:.0f} GB/s); "
+        f"torch formulation {ms_st * 1e3:.0f} us")
+    del g_snap
+    imp = BR.snapkv_key_importance_torch(Qs, Ks, win, 7)
+    del Qs
+    ms_r = time_calls(torch, lambda: BR.retain_blocks_table(imp, w.BS, S, 8, 1, 4, 1), 20)
+    res["retain_us"] = round(ms_r * 1e3, 1)
+    log(f"retain ({w.nb} blocks x {w.Hq} heads): {ms_r * 1e3:.1f} us")
+    frozen = []
+    for l in range(w.L):
+        r = torch.rand(w.Hq, S, device=dev, generator=gen)
+        _, t, n = BR.retain_blocks_table(r, w.BS, S, 8, 1, 4, 1)
+        frozen.append((t, n))
+
+    def frozen_step(l):
+        t, n = BR.frozen_table(frozen[l][0], frozen[l][1], w.nb, w.nb, 1, 4)
+        ops.sparse_decode(w.q[l], w.k[l], w.v[l], t[None], n[None], w.BS, out=w.out[l])
+
+    g_f = capture(torch, frozen_step, w.L, stream)
+    ms_f, _ = time_graph(torch, g_f, 8, 1)
+    res["frozen_decode_us_per_layer"] = round(ms_f * 1e3 / (8 * w.L), 3)
+    log(f"frozen decode (table + sparse decode): {res['frozen_decode_us_per_layer']:.2f} us/layer")
+    del g_f, imp, frozen
+    torch.cuda.empty_cache()
+    return res
+
+
 def model_step(args):
     """Llama-3-70B-shaped decode (80 layers, hidden 8192, 64 q / 8 KV
     heads, head_dim 128, MLP 28672, vocab 128256) with random-init bf16 weights, batch 4,
@@ -533,6 +639,10 @@ def main():
     if not args.no_ragged:
         ragged = ragged_batch(torch, ops, stream, args.seed + 2)
 
+    evict = None
+    if not args.no_evict:
+        evict = evict_bench(torch, ops, w, stream, args.seed + 3, args.h2o_len)
+
     cpu = None
     if not args.no_cpu:
         sec, runs = cpu_baseline(torch, w, args.cpu_seconds)
@@ -570,6 +680,7 @@ def main():
         "cells": cells,
         "ctx_sweep": sweep,
         "ragged_batch": ragged,
+        "eviction": evict,
     }
     print(json.dumps(res), flush=True)
 

@@ -215,7 +215,9 @@ typedef struct {
   int64_t k_stride_h, k_stride_s;
 } adakv_prompt_t;
 
-/* Workspace of adakv_key_importance: one fp32 per (q-head, query >= first_query). */
+/* Workspace of adakv_key_importance (256-byte aligned): one fp32 per
+ * (q-head, query >= first_query), and when those queries are too few to fill
+ * the GPU (a SnapKV window), the partial maxima and sums of a key split. */
 size_t adakv_importance_workspace_bytes(const adakv_prompt_t* p, int32_t first_query);
 
 /* importance[h, j] = sum over the queries i in [first_query, n_tokens) with

@@ -209,3 +209,63 @@ def test_python_errors_mirror_the_reference(lib):
     with pytest.raises(RuntimeError):
         block_sparse_decode(torch.zeros(4, 32), torch.zeros(2, 64, 32), torch.zeros(2, 64, 32),
                             torch.zeros(4, 2, dtype=torch.int32), torch.ones(4, dtype=torch.int32), 16)
+
+
+def test_eviction_entry_points_validate_on_the_host(lib):
+    """The eviction-baseline entry points reject bad arguments before any
+    launch (no device needed)."""
+    P = C.Prompt
+
+    def prompt(**kw):
+        d = dict(q=0x1000, k=0x2000, dtype=C.ADAKV_BF16, Hq=32, Hkv=8, D=128, L=8192,
+                 qsh=8192 * 128, qss=128, ksh=8192 * 128, kss=128)
+        d.update(kw)
+        return P(d["q"], d["k"], d["dtype"], d["Hq"], d["Hkv"], d["D"], d["L"], d["qsh"], d["qss"], d["ksh"],
+                 d["kss"])
+
+    ws = lib.adakv_importance_workspace_bytes
+    assert ws(ctypes.byref(prompt()), 0) == 32 * 8192 * 4
+    assert ws(ctypes.byref(prompt()), 8192 - 32) == 32 * 32 * 4 + 32 * 8 * 32 * 8   # + an 8-way key split
+    assert ws(ctypes.byref(prompt()), 8192) == 0                      # no query left
+    assert ws(ctypes.byref(prompt(D=96)), 0) == 0
+
+    def imp(p, first=0, pitch=8192, nbytes=32 * 8192 * 4, scale=0.088):
+        return lib.adakv_key_importance(ctypes.byref(p), first, ctypes.c_float(scale), ctypes.c_void_p(0x9000),
+                                        pitch, ctypes.c_void_p(0xA000), nbytes, None)
+    assert imp(prompt(Hkv=5)) == C.ADAKV_ERR_SHAPE
+    assert imp(prompt(dtype=9)) == C.ADAKV_ERR_DTYPE
+    assert imp(prompt(D=256)) == C.ADAKV_ERR_UNSUPPORTED
+    assert imp(prompt(q=0x1004)) == C.ADAKV_ERR_VALUE                 # misaligned rows
+    assert imp(prompt(qss=100)) == C.ADAKV_ERR_VALUE
+    assert imp(prompt(), pitch=8000) == C.ADAKV_ERR_SHAPE
+    assert imp(prompt(), first=-1) == C.ADAKV_ERR_VALUE
+    assert imp(prompt(), scale=float("nan")) == C.ADAKV_ERR_VALUE
+    assert imp(prompt(), nbytes=1024) == C.ADAKV_ERR_WORKSPACE
+    assert imp(prompt(k=0)) == C.ADAKV_ERR_NULL
+
+    pool = lib.adakv_importance_pool
+    assert pool(ctypes.c_void_p(0x1000), ctypes.c_void_p(0x100000), 4, 100, 100, 4, None) == C.ADAKV_ERR_VALUE
+    assert pool(ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1100), 4, 100, 100, 7, None) == C.ADAKV_ERR_VALUE
+    assert pool(ctypes.c_void_p(0x1000), ctypes.c_void_p(0x100000), 4, 100, 50, 7, None) == C.ADAKV_ERR_SHAPE
+
+    def retain(n_real=8192, bs=16, mask_pitch=512, budget=8, sel=None):
+        return lib.adakv_retain_blocks(ctypes.c_void_p(0x1000), 32, 1 << 20, n_real, bs, budget, 1, 4, 1,
+                                       ctypes.c_void_p(0x2000), mask_pitch, sel, None)
+    assert retain(n_real=16 * 16385, mask_pitch=16385) == C.ADAKV_ERR_UNSUPPORTED
+    assert retain(mask_pitch=511) == C.ADAKV_ERR_SHAPE
+    assert retain(budget=-1) == C.ADAKV_ERR_VALUE
+    narrow = C.Selection(0x3000, 7, 0x4000)                            # k = 8 does not fit
+    assert retain(sel=ctypes.byref(narrow)) == C.ADAKV_ERR_SHAPE
+
+    frozen = C.Selection(0x3000, 8, 0x4000)
+    out = C.Selection(0x5000, 12, 0x6000)
+    ft = lib.adakv_frozen_table
+    assert ft(ctypes.byref(frozen), 32, 512, 511, 1, 4, ctypes.byref(out), None) == C.ADAKV_ERR_SHAPE
+    assert ft(ctypes.byref(frozen), 32, 512, 600, 1, 4, ctypes.byref(C.Selection(0x5000, 12, 0x6000)),
+              None) == C.ADAKV_ERR_SHAPE                               # needs 8 + 1 + 4
+    assert ft(ctypes.byref(frozen), 32, 512, 70000, 1, 4, ctypes.byref(C.Selection(0x5000, 13, 0x6000)),
+              None) == C.ADAKV_ERR_UNSUPPORTED
+    mt = lib.adakv_mask_table
+    assert mt(ctypes.c_void_p(0x1000), 32, 512, 512, 512, 0, 0, ctypes.byref(C.Selection(0x5000, 511, 0x6000)),
+              None) == C.ADAKV_ERR_SHAPE
+    assert mt(None, 32, 512, 512, 512, 0, 0, ctypes.byref(out), None) == C.ADAKV_ERR_NULL

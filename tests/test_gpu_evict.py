@@ -69,6 +69,8 @@ def _rel(got, want):
     ("fp16", 128, 4, 4, 77),
     ("bf16", 64, 4, 1, 15),
     ("fp32", 128, 2, 1, 1),
+    ("fp32", 64, 2, 1, 3000),         # few query waves: pass 1 splits the keys (3 ranges)
+    ("bf16", 128, 4, 2, 5000),        # window: a 5-way key split
 ])
 @pytest.mark.parametrize("window", [None, 32])
 def test_importance_matches_oracle(dtype, D, Hq, Hkv, L, window):
