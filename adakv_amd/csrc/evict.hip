@@ -61,6 +61,8 @@ struct ImpArgs {
   int pitch;
   int nsplit, klen;            // pass 1 key split: nsplit ranges of klen keys (a multiple of 16)
   float2* part;                // nsplit > 1: partial (max, sum) [Hq, nsplit, L - q0]
+  int hpw;                     // q-heads per wave: 1, or G for a short query range (the wave
+                               // reads its keys once and serves the whole group)
 };
 
 // Workgroup x index -> q-head.  Consecutive workgroups go to the 8 XCDs in
@@ -69,6 +71,11 @@ struct ImpArgs {
 // share their keys through one L2.
 __device__ __forceinline__ int head_of(int bx, int Hq) {
   return (Hq % 8 == 0) ? (bx % 8) * (Hq / 8) + bx / 8 : bx;
+}
+
+// First q-head of the wave's workgroup: the swizzled head, or the group's first.
+__device__ __forceinline__ int first_head(const ImpArgs& a) {
+  return a.hpw == 1 ? head_of(blockIdx.x, a.Hq) : (int)blockIdx.x * a.hpw;
 }
 
 __device__ __forceinline__ void softmax_merge(float& m, float& l, float m2, float l2) {
@@ -128,7 +135,7 @@ __device__ __forceinline__ float4_t tile_dot(const Frag<DT, D>& a, const Frag<DT
 // 4*grp + i of each step; the four lanes of a column merge at the end.
 template <int DT, int D>
 __global__ __launch_bounds__(kEvNT) void importance_lse_kernel(ImpArgs a) {
-  const int h = head_of(blockIdx.x, a.Hq);
+  const int h0 = first_head(a);
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const int col = lane & 15, grp = lane >> 4;
   const int nq = a.L - a.q0;
@@ -136,61 +143,74 @@ __global__ __launch_bounds__(kEvNT) void importance_lse_kernel(ImpArgs a) {
   // the last queries see the most keys: dispatched first
   const int qw = ((nqc - 1 - (int)blockIdx.y / a.nsplit) * (kEvNT / kWave) + w) * kEvRows;
   if (qw >= nq) return;                                   // uniform over the wave; no barriers below
-  const char* qb = a.q + (int64_t)h * a.qsh;
-  const char* kb = a.k + (int64_t)(h / a.G) * a.ksh;
-  Frag<DT, D> qf[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) qf[t].load(qb + (int64_t)min(a.q0 + qw + 16 * t + col, a.L - 1) * a.qss, grp);
+  const char* kb = a.k + (int64_t)(h0 / a.G) * a.ksh;
   const int qlast = min(a.q0 + qw + kEvRows, a.L) - 1;
   const int jb = split * a.klen, je = min(jb + a.klen, qlast + 1);
-  float m[4], l[4];
+  const int ntile = min(4, (nq - qw + 15) / 16);          // tiles past the last query are skipped
+  for (int hh = 0; hh < a.hpw; ++hh) {
+    const int h = h0 + hh;
+    const char* qb = a.q + (int64_t)h * a.qsh;
+    Frag<DT, D> qf[4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) { m[t] = -INFINITY; l[t] = 0.f; }
-  for (int j0 = jb; j0 < je; j0 += 16) {
+    for (int t = 0; t < 4; ++t) qf[t].load(qb + (int64_t)min(a.q0 + qw + 16 * t + col, a.L - 1) * a.qss, grp);
+    float m[4], l[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) { m[t] = -INFINITY; l[t] = 0.f; }
+    // keys of the next step are loaded before this step's products
     Frag<DT, D> kf;
-    kf.load(kb + (int64_t)min(j0 + col, a.L - 1) * a.kss, grp);
+    if (jb < je) kf.load(kb + (int64_t)min(jb + col, a.L - 1) * a.kss, grp);
+    for (int j0 = jb; j0 < je; j0 += 16) {
+      Frag<DT, D> kn;
+      if (j0 + 16 < je) kn.load(kb + (int64_t)min(j0 + 16 + col, a.L - 1) * a.kss, grp);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (t >= ntile) break;                            // uniform over the wave
+        const float4_t s = tile_dot(kf, qf[t]);
+        const int qi = a.q0 + qw + 16 * t + col;
+        float z[4], mx = m[t];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          z[i] = (j0 + 4 * grp + i <= qi) ? s[i] * a.c2 : -INFINITY;
+          mx = fmaxf(mx, z[i]);
+        }
+        if (mx != -INFINITY) {
+          float acc = m[t] == -INFINITY ? 0.f : l[t] * __builtin_amdgcn_exp2f(m[t] - mx);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc += __builtin_amdgcn_exp2f(z[i] - mx);   // exp2(-inf) = 0
+          l[t] = acc;
+          m[t] = mx;
+        }
+      }
+      kf = kn;
+    }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const float4_t s = tile_dot(kf, qf[t]);
-      const int qi = a.q0 + qw + 16 * t + col;
-      float z[4], mx = m[t];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        z[i] = (j0 + 4 * grp + i <= qi) ? s[i] * a.c2 : -INFINITY;
-        mx = fmaxf(mx, z[i]);
+      for (int o = 16; o <= 32; o <<= 1) softmax_merge(m[t], l[t], __shfl_xor(m[t], o), __shfl_xor(l[t], o));
+      const int qo = qw + 16 * t + col;
+      if (grp == 0 && qo < nq) {
+        if (a.nsplit == 1) a.lse[(int64_t)h * nq + qo] = m[t] + log2f(l[t]);
+        else a.part[((int64_t)h * a.nsplit + split) * nq + qo] = make_float2(m[t], l[t]);
       }
-      if (mx != -INFINITY) {
-        float acc = m[t] == -INFINITY ? 0.f : l[t] * __builtin_amdgcn_exp2f(m[t] - mx);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc += __builtin_amdgcn_exp2f(z[i] - mx);   // exp2(-inf) = 0
-        l[t] = acc;
-        m[t] = mx;
-      }
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-#pragma unroll
-    for (int o = 16; o <= 32; o <<= 1) softmax_merge(m[t], l[t], __shfl_xor(m[t], o), __shfl_xor(l[t], o));
-    const int qo = qw + 16 * t + col;
-    if (grp == 0 && qo < nq) {
-      if (a.nsplit == 1) a.lse[(int64_t)h * nq + qo] = m[t] + log2f(l[t]);
-      else a.part[((int64_t)h * a.nsplit + split) * nq + qo] = make_float2(m[t], l[t]);
     }
   }
 }
 
-// Pass 1 with a key split: lse of each (q-head, query) from its partials.
+// Pass 1 with a key split: lse of each (q-head, query) from its partials, one
+// wave per (q-head, query), the lanes striding over the splits.
 __global__ __launch_bounds__(256) void importance_merge_kernel(ImpArgs a) {
   const int nq = a.L - a.q0;
-  const int qo = blockIdx.x * 256 + threadIdx.x, h = blockIdx.y;
-  if (qo >= nq) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int qo = blockIdx.x * (256 / kWave) + threadIdx.x / kWave, h = blockIdx.y;
+  if (qo >= nq) return;                                   // uniform over the wave
   float m = -INFINITY, l = 0.f;
-  for (int s = 0; s < a.nsplit; ++s) {
+  for (int s = lane; s < a.nsplit; s += kWave) {
     const float2 p = a.part[((int64_t)h * a.nsplit + s) * nq + qo];
     softmax_merge(m, l, p.x, p.y);
   }
-  a.lse[(int64_t)h * nq + qo] = m + log2f(l);
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) softmax_merge(m, l, __shfl_xor(m, o), __shfl_xor(l, o));
+  if (lane == 0) a.lse[(int64_t)h * nq + qo] = m + log2f(l);
 }
 
 // ---- pass 2: column sums ------------------------------------------------------
@@ -200,50 +220,65 @@ __global__ __launch_bounds__(256) void importance_merge_kernel(ImpArgs a) {
 // summed at the end.
 template <int DT, int D>
 __global__ __launch_bounds__(kEvNT) void importance_colsum_kernel(ImpArgs a) {
-  const int h = head_of(blockIdx.x, a.Hq);
+  const int h0 = first_head(a);
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const int col = lane & 15, grp = lane >> 4;
   const int nq = a.L - a.q0;
   const int kw = (blockIdx.y * (kEvNT / kWave) + w) * kEvRows;
   if (kw >= a.L) return;                                  // uniform over the wave; no barriers below
-  const char* qb = a.q + (int64_t)h * a.qsh;
-  const char* kb = a.k + (int64_t)(h / a.G) * a.ksh;
-  const float* lse = a.lse + (int64_t)h * nq;
+  const char* kb = a.k + (int64_t)(h0 / a.G) * a.ksh;
   Frag<DT, D> kf[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) kf[t].load(kb + (int64_t)min(kw + 16 * t + col, a.L - 1) * a.kss, grp);
-  float acc[4][4];
+  const int i_begin = max(kw, a.q0);
+  for (int hh = 0; hh < a.hpw; ++hh) {
+    const int h = h0 + hh;
+    const char* qb = a.q + (int64_t)h * a.qsh;
+    const float* lse = a.lse + (int64_t)h * nq;
+    float acc[4][4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[t][i] = 0.f;
-  for (int i0 = max(kw, a.q0); i0 < a.L; i0 += 16) {
-    const int qi = i0 + col;
-    const bool qv = qi < a.L;
+      for (int i = 0; i < 4; ++i) acc[t][i] = 0.f;
+    // queries of the next step (and their lse) are loaded before this step's products
     Frag<DT, D> qf;
-    qf.load(qb + (int64_t)min(qi, a.L - 1) * a.qss, grp);
-    const float ls = qv ? lse[qi - a.q0] : INFINITY;       // an absent query adds exp2(-inf) = 0
+    float ls = INFINITY;                                  // an absent query adds exp2(-inf) = 0
+    if (i_begin < a.L) {
+      qf.load(qb + (int64_t)min(i_begin + col, a.L - 1) * a.qss, grp);
+      if (i_begin + col < a.L) ls = lse[i_begin + col - a.q0];
+    }
+    for (int i0 = i_begin; i0 < a.L; i0 += 16) {
+      const int qi = i0 + col;
+      Frag<DT, D> qn;
+      float ln = INFINITY;
+      if (i0 + 16 < a.L) {
+        qn.load(qb + (int64_t)min(qi + 16, a.L - 1) * a.qss, grp);
+        if (qi + 16 < a.L) ln = lse[qi + 16 - a.q0];
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float4_t s = tile_dot(kf[t], qf);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kj = kw + 16 * t + 4 * grp + i;
+          acc[t][i] += (kj <= qi) ? __builtin_amdgcn_exp2f(s[i] * a.c2 - ls) : 0.f;
+        }
+      }
+      qf = qn;
+      ls = ln;
+    }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const float4_t s = tile_dot(kf[t], qf);
+      float r[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kj = kw + 16 * t + 4 * grp + i;
-        acc[t][i] += (kj <= qi) ? __builtin_amdgcn_exp2f(s[i] * a.c2 - ls) : 0.f;
+      for (int i = 0; i < 4; ++i) r[i] = group_sum<16>(acc[t][i]);
+      const int kj = kw + 16 * t + 4 * grp;
+      if (col == 0) {
+        float* out = a.imp + (int64_t)h * a.pitch;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (kj + i < a.L) out[kj + i] = r[i];
       }
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    float r[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = group_sum<16>(acc[t][i]);
-    const int kj = kw + 16 * t + 4 * grp;
-    if (col == 0) {
-      float* out = a.imp + (int64_t)h * a.pitch;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (kj + i < a.L) out[kj + i] = r[i];
     }
   }
 }
@@ -387,19 +422,25 @@ __global__ __launch_bounds__(kUnionNT) void union_table_kernel(UnionArgs a) {
   table_from_bits<kUnionNT>(bits, a.n, a.table + (int64_t)h * a.width, a.width, a.lens + h, scan);
 }
 
+// A short query range (at most 256 queries: SnapKV's window) is served by
+// waves that each take a whole KV group: the keys of a wave are read once for
+// its G q-heads.
+constexpr int kGroupedQueries = 256;
+int heads_per_wave(int G, int nq) { return nq <= kGroupedQueries ? G : 1; }
+
 // Pass-1 key splits: one per query-chunk wave while those waves fill the GPU
-// (H2O); otherwise (few queries: SnapKV's window) enough splits for about
-// 2048 waves, each over at least 1024 keys.
-int lse_splits(int Hq, int nq, int L) {
-  const int64_t waves = (int64_t)Hq * ((nq + kEvRows - 1) / kEvRows);
+// (H2O); otherwise (few queries) enough splits for about 4096 waves, each over
+// at least 256 keys.
+int lse_splits(int Hq, int G, int nq, int L) {
+  const int64_t waves = (int64_t)(Hq / heads_per_wave(G, nq)) * ((nq + kEvRows - 1) / kEvRows);
   if (waves >= 1024) return 1;
-  return (int)std::max<int64_t>(1, std::min<int64_t>((2048 + waves - 1) / waves, (L + 1023) / 1024));
+  return (int)std::max<int64_t>(1, std::min<int64_t>((4096 + waves - 1) / waves, (L + 255) / 256));
 }
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-size_t importance_ws(int Hq, int nq, int L) {
-  const int ns = lse_splits(Hq, nq, L);
+size_t importance_ws(int Hq, int G, int nq, int L) {
+  const int ns = lse_splits(Hq, G, nq, L);
   const size_t lse = align256((size_t)Hq * nq * sizeof(float));
   return ns == 1 ? lse : lse + (size_t)Hq * ns * nq * sizeof(float2);
 }
@@ -408,15 +449,16 @@ template <int DT>
 hipError_t launch_importance_dt(ImpArgs a, int D, hipStream_t s) {
   constexpr int kRowsPerGroup = kEvNT / kWave * kEvRows;
   const int nq = a.L - a.q0;
-  a.nsplit = lse_splits(a.Hq, nq, a.L);
+  a.hpw = heads_per_wave(a.G, nq);
+  a.nsplit = lse_splits(a.Hq, a.G, nq, a.L);
   a.klen = (a.L + a.nsplit - 1) / a.nsplit;
   a.klen = (a.klen + 15) / 16 * 16;
   a.part = reinterpret_cast<float2*>(reinterpret_cast<char*>(a.lse) + align256((size_t)a.Hq * nq * sizeof(float)));
-  const dim3 g1(a.Hq, ((nq + kRowsPerGroup - 1) / kRowsPerGroup) * a.nsplit);
-  const dim3 g2(a.Hq, (a.L + kRowsPerGroup - 1) / kRowsPerGroup);
+  const dim3 g1(a.Hq / a.hpw, ((nq + kRowsPerGroup - 1) / kRowsPerGroup) * a.nsplit);
+  const dim3 g2(a.Hq / a.hpw, (a.L + kRowsPerGroup - 1) / kRowsPerGroup);
   if (D == 64) importance_lse_kernel<DT, 64><<<g1, kEvNT, 0, s>>>(a);
   else importance_lse_kernel<DT, 128><<<g1, kEvNT, 0, s>>>(a);
-  if (a.nsplit > 1) importance_merge_kernel<<<dim3((nq + 255) / 256, a.Hq), 256, 0, s>>>(a);
+  if (a.nsplit > 1) importance_merge_kernel<<<dim3((nq + 3) / 4, a.Hq), 256, 0, s>>>(a);
   if (D == 64) importance_colsum_kernel<DT, 64><<<g2, kEvNT, 0, s>>>(a);
   else importance_colsum_kernel<DT, 128><<<g2, kEvNT, 0, s>>>(a);
   return hipGetLastError();
@@ -455,7 +497,7 @@ extern "C" {
 
 size_t adakv_importance_workspace_bytes(const adakv_prompt_t* p, int32_t first_query) {
   if (check_prompt(p) != ADAKV_OK || first_query < 0 || first_query >= p->n_tokens) return 0;
-  return importance_ws(p->n_q_heads, p->n_tokens - first_query, p->n_tokens);
+  return importance_ws(p->n_q_heads, p->n_q_heads / p->n_kv_heads, p->n_tokens - first_query, p->n_tokens);
 }
 
 int adakv_key_importance(const adakv_prompt_t* p, int32_t first_query, float sm_scale, float* importance,
@@ -478,7 +520,7 @@ int adakv_key_importance(const adakv_prompt_t* p, int32_t first_query, float sm_
   a.c2 = (float)((double)sm_scale * 1.4426950408889634);
   a.lse = reinterpret_cast<float*>(ws);
   a.imp = importance; a.pitch = pitch;
-  a.nsplit = 1; a.klen = p->n_tokens; a.part = nullptr;   // set by the launcher
+  a.nsplit = 1; a.klen = p->n_tokens; a.part = nullptr; a.hpw = 1;   // set by the launcher
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   switch (p->dtype) {
