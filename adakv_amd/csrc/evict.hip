@@ -139,59 +139,70 @@ __global__ __launch_bounds__(kEvNT) void importance_lse_kernel(ImpArgs a) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const int col = lane & 15, grp = lane >> 4;
   const int nq = a.L - a.q0;
-  const int split = blockIdx.y % a.nsplit, nqc = gridDim.y / a.nsplit;
-  // the last queries see the most keys: dispatched first
-  const int qw = ((nqc - 1 - (int)blockIdx.y / a.nsplit) * (kEvNT / kWave) + w) * kEvRows;
-  if (qw >= nq) return;                                   // uniform over the wave; no barriers below
+  // The wave's four resident tiles are four consecutive (q-head, 16-query tile)
+  // pairs of its q-heads (one head, or a KV group's heads for a short query
+  // range); waves -> (pair group, key split), splits fastest, the pair groups
+  // holding the last queries (the most keys) dispatched first.
+  const int nqt = (nq + 15) / 16;
+  const int npairs = a.hpw * nqt;
+  const int ngroups = (npairs + 3) / 4;
+  const int gw = (int)blockIdx.y * (kEvNT / kWave) + w;
+  if (gw >= ngroups * a.nsplit) return;                   // uniform over the wave; no barriers below
+  const int split = gw % a.nsplit;
+  const int pg = ngroups - 1 - gw / a.nsplit;
   const char* kb = a.k + (int64_t)(h0 / a.G) * a.ksh;
-  const int qlast = min(a.q0 + qw + kEvRows, a.L) - 1;
+  int hs[4], qrow[4];
+  bool live[4];
+  int qlast = 0;
+  Frag<DT, D> qf[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int p = pg * 4 + t;
+    live[t] = p < npairs;                                 // uniform over the wave
+    hs[t] = h0 + (live[t] ? p / nqt : 0);
+    qrow[t] = a.q0 + 16 * (live[t] ? p % nqt : 0);
+    if (live[t]) qlast = max(qlast, min(qrow[t] + 15, a.L - 1));
+    qf[t].load(a.q + (int64_t)hs[t] * a.qsh + (int64_t)min(qrow[t] + col, a.L - 1) * a.qss, grp);
+  }
   const int jb = split * a.klen, je = min(jb + a.klen, qlast + 1);
-  const int ntile = min(4, (nq - qw + 15) / 16);          // tiles past the last query are skipped
-  for (int hh = 0; hh < a.hpw; ++hh) {
-    const int h = h0 + hh;
-    const char* qb = a.q + (int64_t)h * a.qsh;
-    Frag<DT, D> qf[4];
+  float m[4], l[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) qf[t].load(qb + (int64_t)min(a.q0 + qw + 16 * t + col, a.L - 1) * a.qss, grp);
-    float m[4], l[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) { m[t] = -INFINITY; l[t] = 0.f; }
-    // keys of the next step are loaded before this step's products
-    Frag<DT, D> kf;
-    if (jb < je) kf.load(kb + (int64_t)min(jb + col, a.L - 1) * a.kss, grp);
-    for (int j0 = jb; j0 < je; j0 += 16) {
-      Frag<DT, D> kn;
-      if (j0 + 16 < je) kn.load(kb + (int64_t)min(j0 + 16 + col, a.L - 1) * a.kss, grp);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if (t >= ntile) break;                            // uniform over the wave
-        const float4_t s = tile_dot(kf, qf[t]);
-        const int qi = a.q0 + qw + 16 * t + col;
-        float z[4], mx = m[t];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          z[i] = (j0 + 4 * grp + i <= qi) ? s[i] * a.c2 : -INFINITY;
-          mx = fmaxf(mx, z[i]);
-        }
-        if (mx != -INFINITY) {
-          float acc = m[t] == -INFINITY ? 0.f : l[t] * __builtin_amdgcn_exp2f(m[t] - mx);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc += __builtin_amdgcn_exp2f(z[i] - mx);   // exp2(-inf) = 0
-          l[t] = acc;
-          m[t] = mx;
-        }
-      }
-      kf = kn;
-    }
+  for (int t = 0; t < 4; ++t) { m[t] = -INFINITY; l[t] = 0.f; }
+  // keys of the next step are loaded before this step's products
+  Frag<DT, D> kf;
+  if (jb < je) kf.load(kb + (int64_t)min(jb + col, a.L - 1) * a.kss, grp);
+  for (int j0 = jb; j0 < je; j0 += 16) {
+    Frag<DT, D> kn;
+    if (j0 + 16 < je) kn.load(kb + (int64_t)min(j0 + 16 + col, a.L - 1) * a.kss, grp);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
+      if (!live[t]) continue;                             // uniform over the wave
+      const float4_t s = tile_dot(kf, qf[t]);
+      const int qi = qrow[t] + col;
+      float z[4], mx = m[t];
 #pragma unroll
-      for (int o = 16; o <= 32; o <<= 1) softmax_merge(m[t], l[t], __shfl_xor(m[t], o), __shfl_xor(l[t], o));
-      const int qo = qw + 16 * t + col;
-      if (grp == 0 && qo < nq) {
-        if (a.nsplit == 1) a.lse[(int64_t)h * nq + qo] = m[t] + log2f(l[t]);
-        else a.part[((int64_t)h * a.nsplit + split) * nq + qo] = make_float2(m[t], l[t]);
+      for (int i = 0; i < 4; ++i) {
+        z[i] = (j0 + 4 * grp + i <= qi) ? s[i] * a.c2 : -INFINITY;
+        mx = fmaxf(mx, z[i]);
       }
+      if (mx != -INFINITY) {
+        float acc = m[t] == -INFINITY ? 0.f : l[t] * __builtin_amdgcn_exp2f(m[t] - mx);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc += __builtin_amdgcn_exp2f(z[i] - mx);   // exp2(-inf) = 0
+        l[t] = acc;
+        m[t] = mx;
+      }
+    }
+    kf = kn;
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+#pragma unroll
+    for (int o = 16; o <= 32; o <<= 1) softmax_merge(m[t], l[t], __shfl_xor(m[t], o), __shfl_xor(l[t], o));
+    const int qo = qrow[t] - a.q0 + col;
+    if (live[t] && grp == 0 && qo < nq) {
+      if (a.nsplit == 1) a.lse[(int64_t)hs[t] * nq + qo] = m[t] + log2f(l[t]);
+      else a.part[((int64_t)hs[t] * a.nsplit + split) * nq + qo] = make_float2(m[t], l[t]);
     }
   }
 }
@@ -428,13 +439,16 @@ __global__ __launch_bounds__(kUnionNT) void union_table_kernel(UnionArgs a) {
 constexpr int kGroupedQueries = 256;
 int heads_per_wave(int G, int nq) { return nq <= kGroupedQueries ? G : 1; }
 
-// Pass-1 key splits: one per query-chunk wave while those waves fill the GPU
-// (H2O); otherwise (few queries) enough splits for about 4096 waves, each over
-// at least 256 keys.
+// Pass-1 key splits: none while the query waves fill the GPU (H2O); otherwise
+// (few queries) enough splits for about 8192 waves, each over at least 256 keys.
+int lse_pair_groups(int G, int nq) {
+  return (heads_per_wave(G, nq) * ((nq + 15) / 16) + 3) / 4;
+}
+
 int lse_splits(int Hq, int G, int nq, int L) {
-  const int64_t waves = (int64_t)(Hq / heads_per_wave(G, nq)) * ((nq + kEvRows - 1) / kEvRows);
+  const int64_t waves = (int64_t)(Hq / heads_per_wave(G, nq)) * lse_pair_groups(G, nq);
   if (waves >= 1024) return 1;
-  return (int)std::max<int64_t>(1, std::min<int64_t>((4096 + waves - 1) / waves, (L + 255) / 256));
+  return (int)std::max<int64_t>(1, std::min<int64_t>((8192 + waves - 1) / waves, (L + 255) / 256));
 }
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
@@ -454,7 +468,8 @@ hipError_t launch_importance_dt(ImpArgs a, int D, hipStream_t s) {
   a.klen = (a.L + a.nsplit - 1) / a.nsplit;
   a.klen = (a.klen + 15) / 16 * 16;
   a.part = reinterpret_cast<float2*>(reinterpret_cast<char*>(a.lse) + align256((size_t)a.Hq * nq * sizeof(float)));
-  const dim3 g1(a.Hq / a.hpw, ((nq + kRowsPerGroup - 1) / kRowsPerGroup) * a.nsplit);
+  const int waves1 = lse_pair_groups(a.G, nq) * a.nsplit;
+  const dim3 g1(a.Hq / a.hpw, (waves1 + kEvNT / kWave - 1) / (kEvNT / kWave));
   const dim3 g2(a.Hq / a.hpw, (a.L + kRowsPerGroup - 1) / kRowsPerGroup);
   if (D == 64) importance_lse_kernel<DT, 64><<<g1, kEvNT, 0, s>>>(a);
   else importance_lse_kernel<DT, 128><<<g1, kEvNT, 0, s>>>(a);
