@@ -241,56 +241,67 @@ __global__ __launch_bounds__(kEvNT) void importance_colsum_kernel(ImpArgs a) {
   Frag<DT, D> kf[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) kf[t].load(kb + (int64_t)min(kw + 16 * t + col, a.L - 1) * a.kss, grp);
-  const int i_begin = max(kw, a.q0);
-  for (int hh = 0; hh < a.hpw; ++hh) {
-    const int h = h0 + hh;
-    const char* qb = a.q + (int64_t)h * a.qsh;
-    const float* lse = a.lse + (int64_t)h * nq;
-    float acc[4][4];
+  // (q-head, 16-query step) pairs in one loop -- the q-heads of the wave one
+  // after another -- so that the next pair's queries and lse are in flight
+  // while this pair's products run, across head boundaries too
+  const int i_begin = max(kw, a.q0);                      // < L: kw < L and q0 < L
+  auto q_row = [&](int hh, int i0) {
+    return a.q + (int64_t)(h0 + hh) * a.qsh + (int64_t)min(i0 + col, a.L - 1) * a.qss;
+  };
+  auto lse_of = [&](int hh, int i0) {
+    const int qi = i0 + col;
+    return qi < a.L ? a.lse[(int64_t)(h0 + hh) * nq + qi - a.q0] : INFINITY;   // absent: exp2(-inf) = 0
+  };
+  float acc[4][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+  for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[t][i] = 0.f;
-    // queries of the next step (and their lse) are loaded before this step's products
-    Frag<DT, D> qf;
-    float ls = INFINITY;                                  // an absent query adds exp2(-inf) = 0
-    if (i_begin < a.L) {
-      qf.load(qb + (int64_t)min(i_begin + col, a.L - 1) * a.qss, grp);
-      if (i_begin + col < a.L) ls = lse[i_begin + col - a.q0];
+    for (int i = 0; i < 4; ++i) acc[t][i] = 0.f;
+  Frag<DT, D> qf;
+  qf.load(q_row(0, i_begin), grp);
+  float ls = lse_of(0, i_begin);
+  for (int hh = 0, i0 = i_begin; hh < a.hpw;) {
+    // the pair after this one: the next 16 queries, or the next head's first
+    const bool last_of_head = i0 + 16 >= a.L;
+    const int nh = last_of_head ? hh + 1 : hh, ni = last_of_head ? i_begin : i0 + 16;
+    Frag<DT, D> qn;
+    float ln = INFINITY;
+    if (nh < a.hpw) {
+      qn.load(q_row(nh, ni), grp);
+      ln = lse_of(nh, ni);
     }
-    for (int i0 = i_begin; i0 < a.L; i0 += 16) {
-      const int qi = i0 + col;
-      Frag<DT, D> qn;
-      float ln = INFINITY;
-      if (i0 + 16 < a.L) {
-        qn.load(qb + (int64_t)min(qi + 16, a.L - 1) * a.qss, grp);
-        if (qi + 16 < a.L) ln = lse[qi + 16 - a.q0];
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float4_t s = tile_dot(kf[t], qf);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kj = kw + 16 * t + 4 * grp + i;
-          acc[t][i] += (kj <= qi) ? __builtin_amdgcn_exp2f(s[i] * a.c2 - ls) : 0.f;
-        }
-      }
-      qf = qn;
-      ls = ln;
-    }
+    const int qi = i0 + col;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      float r[4];
+      const float4_t s = tile_dot(kf[t], qf);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) r[i] = group_sum<16>(acc[t][i]);
-      const int kj = kw + 16 * t + 4 * grp;
-      if (col == 0) {
-        float* out = a.imp + (int64_t)h * a.pitch;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (kj + i < a.L) out[kj + i] = r[i];
+      for (int i = 0; i < 4; ++i) {
+        const int kj = kw + 16 * t + 4 * grp + i;
+        acc[t][i] += (kj <= qi) ? __builtin_amdgcn_exp2f(s[i] * a.c2 - ls) : 0.f;
       }
     }
+    if (last_of_head) {                                   // the head's sums out
+      float* out = a.imp + (int64_t)(h0 + hh) * a.pitch;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        float r[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          r[i] = group_sum<16>(acc[t][i]);
+          acc[t][i] = 0.f;
+        }
+        const int kj = kw + 16 * t + 4 * grp;
+        if (col == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (kj + i < a.L) out[kj + i] = r[i];
+        }
+      }
+    }
+    qf = qn;
+    ls = ln;
+    hh = nh;
+    i0 = ni;
   }
 }
 
