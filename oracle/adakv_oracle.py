@@ -22,10 +22,14 @@ Numerics follow the reference's NumPy 2 dtype rules exactly:
 * selection ranks fp64 copies of the scores, sink/local forced via ``+inf``
   (selector.py:44-60).
 
-Pinning (see tests/test_oracle_golden.py and tests/test_oracle_properties.py):
-golden vectors written by the real reference in this container
-(tests/golden/make_golden.py) pin scores, weights, budgets, masks and outputs;
-closed forms / brute force pin the centroid, the selection and the attention.
+Pinning (see tests/test_oracle_golden.py, tests/test_oracle_properties.py and
+tests/test_oracle_evict.py): golden vectors written by the real reference in
+this container (tests/golden/make_golden.py) pin scores, weights, budgets,
+masks and outputs; closed forms / brute force pin the centroid, the selection
+and the attention; the eviction baselines (key importance, pool, retention,
+frozen tables and attention) are pinned by closed forms (column totals, the
+last key's weight), a brute force, SciPy's maximum_filter1d, a sort, and the
+reference's own CPU scenarios.
 """
 from __future__ import annotations
 
