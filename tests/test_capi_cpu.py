@@ -225,7 +225,8 @@ def test_eviction_entry_points_validate_on_the_host(lib):
 
     ws = lib.adakv_importance_workspace_bytes
     assert ws(ctypes.byref(prompt()), 0) == 32 * 8192 * 4
-    assert ws(ctypes.byref(prompt()), 8192 - 32) == 32 * 32 * 4 + 32 * 8 * 32 * 8   # + an 8-way key split
+    # 32 queries, G 4: 8 grouped waves x 2 tile groups = 16 waves, split 32 ways over 8192 keys (256 each)
+    assert ws(ctypes.byref(prompt()), 8192 - 32) == 32 * 32 * 4 + 32 * 32 * 32 * 8
     assert ws(ctypes.byref(prompt()), 8192) == 0                      # no query left
     assert ws(ctypes.byref(prompt(D=96)), 0) == 0
 
