@@ -26,7 +26,8 @@ namespace adakv {
 namespace {
 
 constexpr int kNT = 256;
-constexpr int kScoreTiles = 4;   // 16-row summary tiles per wave of the matrix-core scan
+constexpr int kScoreTiles = 4;   // 16-row summary tiles per wave of the matrix-core scan (at most)
+constexpr int kScoreFill = 256;  // workgroups the scan aims for (one per CU) before it shortens its waves
 
 __device__ __forceinline__ float round_to(float x, int dt) {
   if (dt == ADAKV_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(x));
@@ -221,20 +222,20 @@ __device__ void score_chunk_valu(const ScoreArgs& a, int b, int kvh, int unit, i
 }
 
 // bf16 / fp16 centroids on the matrix cores: S = C . Q^T with
-// v_mfma_f32_16x16x32 -- a wave holds 4 tiles of 16 centroid rows in the
+// v_mfma_f32_16x16x32 -- a wave holds TPW tiles of 16 centroid rows in the
 // A-operand layout (lane l: row l%16, a contiguous D/2-byte slice of it, all
 // loads issued at once), the group's q-heads, zero-padded to 16, form the B
 // operand.  Result lane (col, grp) holds the scores of rows 4*grp .. +3 of a
 // tile for head col: written as 16-byte stores, and reduced over the wave's
-// 64 rows (one sub-chunk) into that head's softmax partial; the 4 waves'
+// 16 * TPW rows (one sub-chunk) into that head's softmax partial; the 4 waves'
 // partials are merged through LDS into the workgroup's record.
-template <int CDT, int D, int GMAX, bool MM>
+template <int CDT, int D, int GMAX, bool MM, int TPW>
 __device__ void score_chunk_mfma(const ScoreArgs& a, int b, int kvh, int unit, int nb, int nrows,
                                  float (*s_pm)[GMAX][4]) {
   static_assert(D % 32 == 0 && GMAX <= 16, "16x16 tiles over head_dim");
   constexpr int KS = D / 32;                // k-steps (16-byte loads per lane per tile)
   constexpr int QS = MM ? KS / 2 : KS;      // distinct q slices (a minmax row repeats q: max(q,0), min(q,0))
-  constexpr int TPW = kScoreTiles;          // tiles per wave
+  // TPW: tiles per wave
   constexpr int RPW = 16 * TPW;             // rows per wave = rows per sub-chunk
   constexpr int NWV = kNT / kWave;
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
@@ -408,7 +409,7 @@ __device__ void score_chunk_mfma(const ScoreArgs& a, int b, int kvh, int unit, i
 // 1-D grid: first n_app workgroups per (sequence, KV head) for the appended
 // blocks (dispatched first: their dependent K loads are the longest chain),
 // then n_chunks workgroups per (sequence, KV head).
-template <int CDT, int D, int GMAX, bool MM>
+template <int CDT, int D, int GMAX, bool MM, int TPW>
 __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
   constexpr bool kMfma = CDT != ADAKV_F32;
   constexpr int CBV = (kNT / kWave) * (kWave / (D / Elt<CDT>::kPerVec)) * 4;   // VALU rows per workgroup
@@ -441,30 +442,55 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
   }
   const int nrows = min(nb, first_app);     // appended blocks are scored by their own workgroups
   if constexpr (kMfma) {
-    score_chunk_mfma<CDT, D, GMAX, MM>(a, b, kvh, unit, nb, nrows, s_pm);
+    score_chunk_mfma<CDT, D, GMAX, MM, TPW>(a, b, kvh, unit, nb, nrows, s_pm);
   } else {
     if (unit * CBV >= nrows) return;
     score_chunk_valu<CDT, D, GMAX, MM>(a, b, kvh, unit, nb, nrows, s_q, s_sc);
   }
 }
 
+template <int CDT, int D, bool MM, int TPW>
+void launch_score_g(const ScoreArgs& a, dim3 grid, hipStream_t s) {
+  if (a.G <= 1) hipLaunchKernelGGL((score_kernel<CDT, D, 1, MM, TPW>), grid, dim3(kNT), 0, s, a);
+  else if (a.G <= 2) hipLaunchKernelGGL((score_kernel<CDT, D, 2, MM, TPW>), grid, dim3(kNT), 0, s, a);
+  else if (a.G <= 4) hipLaunchKernelGGL((score_kernel<CDT, D, 4, MM, TPW>), grid, dim3(kNT), 0, s, a);
+  else hipLaunchKernelGGL((score_kernel<CDT, D, 8, MM, TPW>), grid, dim3(kNT), 0, s, a);
+}
+
+// Tiles per wave of the matrix-core scan: kScoreTiles, halved while the grid
+// would hold fewer than kScoreFill workgroups (short contexts: more, shorter
+// waves, and finer sub-chunk maxima for the selection's threshold), as long as
+// the records still fit their pitch.
+inline int score_tiles(const ScoreArgs& a) {
+  auto chunks = [&](int tpw) { return (a.max_blocks + 64 * tpw - 1) / (64 * tpw); };
+  int tpw = kScoreTiles;
+  while (tpw > 1 && (int64_t)chunks(tpw) * a.Hkv * a.B < kScoreFill &&
+         (a.parts == nullptr || chunks(tpw / 2) <= a.parts_pitch))
+    tpw /= 2;
+  return tpw;
+}
+
 template <int CDT, int D, bool MM>
 hipError_t launch_score_d(ScoreArgs& a, hipStream_t s) {
+  int tpw = kScoreTiles;
   if constexpr (CDT == ADAKV_F32) {
     constexpr int CB = (kNT / kWave) * (kWave / (D / 4)) * 4;   // rows per workgroup = rows per partial
     a.chunk_rows = CB;
-    a.n_chunks = (a.max_blocks + CB - 1) / CB;
   } else {
-    a.chunk_rows = 4 * 16 * kScoreTiles;                        // 4 waves of 16-row tiles per record
-    a.n_chunks = (a.max_blocks + a.chunk_rows - 1) / a.chunk_rows;
+    tpw = score_tiles(a);
+    a.chunk_rows = 4 * 16 * tpw;                                // 4 waves of 16-row tiles per record
   }
+  a.n_chunks = (a.max_blocks + a.chunk_rows - 1) / a.chunk_rows;
   // blocks holding the newest n_new tokens: at most ceil(n_new / bs) + 1
   a.n_app = a.n_new > 0 ? std::min((a.n_new + a.bs - 1) / a.bs + 1, a.max_blocks) : 0;
   dim3 grid((unsigned)((int64_t)(a.n_app + a.n_chunks) * a.Hkv * a.B));
-  if (a.G <= 1) hipLaunchKernelGGL((score_kernel<CDT, D, 1, MM>), grid, dim3(kNT), 0, s, a);
-  else if (a.G <= 2) hipLaunchKernelGGL((score_kernel<CDT, D, 2, MM>), grid, dim3(kNT), 0, s, a);
-  else if (a.G <= 4) hipLaunchKernelGGL((score_kernel<CDT, D, 4, MM>), grid, dim3(kNT), 0, s, a);
-  else hipLaunchKernelGGL((score_kernel<CDT, D, 8, MM>), grid, dim3(kNT), 0, s, a);
+  if constexpr (CDT == ADAKV_F32) {
+    launch_score_g<CDT, D, MM, kScoreTiles>(a, grid, s);
+  } else {
+    if (tpw == 1) launch_score_g<CDT, D, MM, 1>(a, grid, s);
+    else if (tpw == 2) launch_score_g<CDT, D, MM, 2>(a, grid, s);
+    else launch_score_g<CDT, D, MM, kScoreTiles>(a, grid, s);
+  }
   return hipGetLastError();
 }
 
