@@ -112,7 +112,19 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
 
   const SelectArgs& a = fa.s;
   const DecodeArgs& d = fa.d;
-  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  // XCD-aware placement: workgroups are dealt to the 8 XCDs in turn (linear id
+  // mod 8), so linear id i takes position (i mod 8) * n/8 + i / 8 of the
+  // (sequence, q-head) order: each XCD holds consecutive q-heads -- the heads
+  // of a KV group, the sequences' records and their shared sink, local and
+  // common blocks then meet in one L2.
+  int h, b;
+  {
+    const int n = gridDim.x * gridDim.y, i = blockIdx.y * gridDim.x + blockIdx.x;
+    const int pos = (n & 7) == 0 ? (i & 7) * (n >> 3) + (i >> 3) : i;
+    h = pos % gridDim.x;
+    b = pos / gridDim.x;
+  }
+  const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1), w = tid / kWave;
   const int col = lane & 15, grp = lane >> 4;
   const int Hq = a.Hq;

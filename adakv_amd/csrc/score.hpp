@@ -66,7 +66,7 @@ __device__ __forceinline__ uint32_t pack2_typed(float lo, float hi) {
 // instruction covers one row, coalesced) and reduces them in token order in
 // registers.
 template <int CDT, int KDT, int D, int GMAX, bool MM>
-__device__ void append_block(const ScoreArgs& a, int b, int kvh, int r, int len, float (*s_red)[kNT / kWave]) {
+__device__ __forceinline__ void append_block(const ScoreArgs& a, int b, int kvh, int r, int len, float (*s_red)[kNT / kWave]) {
   constexpr int TB = 16;                       // token rows loaded together
   constexpr int DH = MM ? D / 2 : D;           // head_dim
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
@@ -132,7 +132,7 @@ __device__ __forceinline__ void write_part(const ScoreArgs& a, int b, int h, int
 // read once with 16-byte loads and dotted with the G queries (fp32 FMA, then a
 // DPP butterfly over the lanes sharing the row); one partial per chunk.
 template <int CDT, int D, int GMAX, bool MM>
-__device__ void score_chunk_valu(const ScoreArgs& a, int b, int kvh, int unit, int nb, int nrows,
+__device__ __forceinline__ void score_chunk_valu(const ScoreArgs& a, int b, int kvh, int unit, int nb, int nrows,
                                  float (*s_q)[D], float* s_sc_flat) {
   constexpr int EPV = Elt<CDT>::kPerVec;
   constexpr int EB = Elt<CDT>::kBytes;
@@ -230,7 +230,7 @@ __device__ void score_chunk_valu(const ScoreArgs& a, int b, int kvh, int unit, i
 // 16 * TPW rows (one sub-chunk) into that head's softmax partial; the 4 waves'
 // partials are merged through LDS into the workgroup's record.
 template <int CDT, int D, int GMAX, bool MM, int TPW>
-__device__ void score_chunk_mfma(const ScoreArgs& a, int b, int kvh, int unit, int nb, int nrows,
+__device__ __forceinline__ void score_chunk_mfma(const ScoreArgs& a, int b, int kvh, int unit, int nb, int nrows,
                                  float (*s_pm)[GMAX][4]) {
   static_assert(D % 32 == 0 && GMAX <= 16, "16x16 tiles over head_dim");
   constexpr int KS = D / 32;                // k-steps (16-byte loads per lane per tile)
