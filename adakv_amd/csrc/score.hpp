@@ -429,6 +429,11 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
   }
   kvh = id % a.Hkv;
   b = id / a.Hkv;
+  // Sequence b's chunks are rotated by 8b: workgroups are dealt to XCDs (id
+  // mod 8) and then to an XCD's CUs in turn, so without it a CU would hold
+  // the same chunk indices of every sequence, and in a ragged batch (the high
+  // chunks of short sequences empty) the CUs of the high chunks would idle.
+  if (!app) unit = (unit + 8 * b) % a.n_chunks;
   const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
   const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
   const int first_app = a.n_new > 0 ? max(len - a.n_new, 0) / a.bs : nb;
