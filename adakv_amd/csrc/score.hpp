@@ -337,14 +337,30 @@ __device__ __forceinline__ void score_chunk_mfma(const ScoreArgs& a, int b, int 
     const Bounds bb = budget_bounds(nb, a.cfg);
     const int c_lo = bb.sink, c_hi = nb - bb.local;
     const float tf = (float)fmax(a.cfg.temperature, 1e-6);
-    // branch-free: content and validity are selects, empty rows contribute exp(-inf) = 0
+    // Uniform over the wave: every row of the wave is a content row and holds
+    // a score.  Then the content maximum is sanitize() of the plain maximum
+    // (sanitize is monotone and maps NaN to its lowest value, which fmaxf
+    // skips), and at temperature 1 it is also the softmax maximum: no per-row
+    // selects.  Waves at the sink / local edges or past the scored rows take
+    // the masked path.
+    const bool full = wrow0 >= c_lo && wrow0 + RPW <= min(c_hi, nrows);
+    float mx = -INFINITY;
+    if (full) {
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
+      for (int t = 0; t < TPW; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = wrow0 + 16 * t + 4 * grp + i;
-        const bool cont = (r >= c_lo) & (r < c_hi) & (r < nrows);
-        hi = fmaxf(hi, cont ? sanitize(sc[t][i]) : -INFINITY);
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[t][i]);
+      hi = sanitize(mx);
+    } else {
+      // branch-free: content and validity are selects, empty rows contribute exp(-inf) = 0
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = wrow0 + 16 * t + 4 * grp + i;
+          const bool cont = (r >= c_lo) & (r < c_hi) & (r < nrows);
+          hi = fmaxf(hi, cont ? sanitize(sc[t][i]) : -INFINITY);
+        }
       }
     }
     if (tf != 1.f) {   // temperature: the correctly rounded division only when it is needed (uniform)
@@ -353,13 +369,17 @@ __device__ __forceinline__ void score_chunk_mfma(const ScoreArgs& a, int b, int 
 #pragma unroll
         for (int i = 0; i < 4; ++i) sc[t][i] = __fdiv_rn(sc[t][i], tf);
     }
+    if (full && tf == 1.f) {
+      m = mx;
+    } else {
 #pragma unroll
-    for (int t = 0; t < TPW; ++t)
+      for (int t = 0; t < TPW; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sc[t][i] = (wrow0 + 16 * t + 4 * grp + i < nrows) ? sc[t][i] : -INFINITY;
-        m = fmaxf(m, sc[t][i]);
-      }
+        for (int i = 0; i < 4; ++i) {
+          sc[t][i] = (wrow0 + 16 * t + 4 * grp + i < nrows) ? sc[t][i] : -INFINITY;
+          m = fmaxf(m, sc[t][i]);
+        }
+    }
     LanePair pr = swap16(m);
     m = fmaxf(pr.a, pr.b);
     pr = swap32(m);
