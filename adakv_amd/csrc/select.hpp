@@ -143,8 +143,8 @@ __device__ __forceinline__ double entropy_weight(const SoftPart& p, double lognb
 //   a = #{p > p*} and M their mass; the crossing is the i-th copy of p*,
 //   i = ceil((P - M) / p*), and K* = a + i.
 struct NucleusLds {
-  unsigned long long mass[256];
-  int cnt[256];
+  unsigned long long mass[2][256];   // pass k histograms into buffer k & 1 while the other is cleared
+  int cnt[2][256];
   float fred[16];
   double dred[16];
   unsigned long long qred[16];
@@ -164,36 +164,41 @@ __device__ __forceinline__ unsigned long long wave_excl_scan_u64(unsigned long l
   return inc - x;
 }
 
-// One pass: candidates are the elements with cand(i), of mass mq(i) and digit
-// digit(i) in [0, 256).  With tail_bin, bin 255 is not accumulated: it holds
-// the rest of m_tot / n_tot.  Returns false (uniformly) when the mass never
-// reaches Pq.  On return N.prefix holds the chosen digit appended to `prefix`.
+// One pass (the k-th): candidates are the elements with cand(i), of mass
+// mq(i) and digit digit(i) in [0, 256).  With tail_bin, bin 255 is not
+// accumulated: it holds the rest of m_tot / n_tot.  Returns false (uniformly)
+// when the mass never reaches Pq.  On return N.prefix holds the chosen digit
+// appended to `prefix`.  Histogram buffer k & 1 must be clear on entry; the
+// other buffer is cleared while wave 0 scans this one, for the next pass.
 template <int NT, int IPT, typename Mass, typename Cand, typename Digit>
-__device__ __forceinline__ bool nucleus_pass(NucleusLds& N, Mass mq, Cand cand, Digit digit,
+__device__ __forceinline__ bool nucleus_pass(NucleusLds& N, int k, Mass mq, Cand cand, Digit digit,
                                              unsigned long long Pq, uint32_t prefix, int bits, bool tail_bin,
                                              unsigned long long m_tot, int n_tot) {
+  static_assert(NT >= 2 * kWave, "wave 0 scans while the others clear");
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
-  for (int j = tid; j < 256; j += NT) { N.mass[j] = 0ull; N.cnt[j] = 0; }
-  lds_barrier();
+  unsigned long long* hmass = N.mass[k & 1];
+  int* hcnt = N.cnt[k & 1];
 #pragma unroll
   for (int i = 0; i < IPT; ++i) {
     if (cand(i)) {
       const int d = digit(i);
       if (!(tail_bin && d == 255)) {
-        atomicAdd(&N.mass[d], mq(i));
-        atomicAdd(&N.cnt[d], 1);
+        atomicAdd(&hmass[d], mq(i));
+        atomicAdd(&hcnt[d], 1);
       }
     }
   }
   lds_barrier();
-  if (w == 0) {
+  if (w != 0) {
+    for (int j = tid - kWave; j < 256; j += NT - kWave) { N.mass[(k + 1) & 1][j] = 0ull; N.cnt[(k + 1) & 1][j] = 0; }
+  } else {
     // lane l holds digits 4l .. 4l+3: lane order is digit order
     unsigned long long bm[4], lm = 0ull;
     int bc[4], lc = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      bm[j] = N.mass[4 * lane + j];
-      bc[j] = N.cnt[4 * lane + j];
+      bm[j] = hmass[4 * lane + j];
+      bc[j] = hcnt[4 * lane + j];
       lm += bm[j];
       lc += bc[j];
     }
@@ -272,8 +277,20 @@ __device__ double nucleus_weight(NucleusLds& N, float (&z)[IPT], int nb, float t
   uint32_t dist[IPT];
 #pragma unroll
   for (int i = 0; i < IPT; ++i) dist[i] = base + i < nb ? kmax - __float_as_uint(__fdiv_rn(z[i], s32)) : kNone;
-  auto mq = [&](int i) -> unsigned long long {
+  auto mass_of = [&](int i) -> unsigned long long {
     return (unsigned long long)((double)__uint_as_float(kmax - dist[i]) * kScale);
+  };
+  // with few elements per thread their masses stay in registers, else each
+  // pass recomputes them from dist
+  constexpr bool kKeep = IPT <= 8;
+  unsigned long long mkeep[kKeep ? IPT : 1];
+  if constexpr (kKeep) {
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) mkeep[i] = dist[i] != kNone ? mass_of(i) : 0ull;
+  }
+  auto mq = [&](int i) -> unsigned long long {
+    if constexpr (kKeep) return mkeep[i];
+    else return mass_of(i);
   };
   unsigned long long mloc = 0ull;
 #pragma unroll
@@ -281,6 +298,7 @@ __device__ double nucleus_weight(NucleusLds& N, float (&z)[IPT], int nb, float t
   mloc = wave_sum(mloc);
   if (lane == 0) N.qred[w] = mloc;
   if (tid == 0) { N.m_above = 0ull; N.n_above = 0; }
+  for (int j = tid; j < 256; j += NT) { N.mass[0][j] = 0ull; N.cnt[0][j] = 0; }   // the first pass's histograms
   lds_barrier();
   unsigned long long m_tot = 0ull;
 #pragma unroll
@@ -289,7 +307,7 @@ __device__ double nucleus_weight(NucleusLds& N, float (&z)[IPT], int nb, float t
   const unsigned long long Pq = (unsigned long long)(P * kScale);
   auto valid = [&](int i) { return dist[i] != kNone; };
   // pass 1: 1/16-octave bins below the maximum, the tail in bin 255
-  if (!nucleus_pass<NT, IPT>(N, mq, valid, [&](int i) { return (int)min(dist[i] >> 19, 255u); }, Pq, 0u, 8,
+  if (!nucleus_pass<NT, IPT>(N, 0, mq, valid, [&](int i) { return (int)min(dist[i] >> 19, 255u); }, Pq, 0u, 8,
                              true, m_tot, nb))
     return (double)(nb + 1);                 // the whole mass stays below P
   uint32_t pre = N.prefix;
@@ -300,7 +318,7 @@ __device__ double nucleus_weight(NucleusLds& N, float (&z)[IPT], int nb, float t
 #pragma unroll 1
     for (int ps = 0; ps < 3; ++ps) {
       const int sh = kShift[ps], nbits = kBits[ps];
-      nucleus_pass<NT, IPT>(N, mq, [&](int i) { return valid(i) && (dist[i] >> (sh + nbits)) == pre; },
+      nucleus_pass<NT, IPT>(N, 1 + ps, mq, [&](int i) { return valid(i) && (dist[i] >> (sh + nbits)) == pre; },
                             [&](int i) { return (int)((dist[i] >> sh) & ((1u << nbits) - 1u)); }, Pq, pre,
                             nbits, false, 0ull, 0);
       pre = N.prefix;
@@ -313,7 +331,7 @@ __device__ double nucleus_weight(NucleusLds& N, float (&z)[IPT], int nb, float t
 #pragma unroll 1
     for (int sh = 24; sh >= 0; sh -= 8) {
       const int nbits = sh == 24 ? 7 : 8;
-      nucleus_pass<NT, IPT>(N, mq,
+      nucleus_pass<NT, IPT>(N, (24 - sh) / 8 + 1, mq,
                             [&](int i) {
                               return valid(i) && dist[i] >= kTail && (sh == 24 || (dist[i] >> (sh + 8)) == pre);
                             },
