@@ -118,6 +118,26 @@ def test_config3_needles_128k(avg, cdt):
     _check_output(out[0].float().cpu().numpy(), _ref_selected(q_np, k[0], v[0], table, lens, S))
 
 
+@pytest.mark.parametrize("S", [65536, 100000])
+def test_needles_two_tiles_per_wave(S):
+    """4096 and 6250 blocks per KV head: the matrix-core scan runs 2 tiles per
+    wave (4 from 7937 blocks on, 1 below 3969, at 8 KV heads and batch 1), so
+    its records cover 128 rows."""
+    ops = _ops()
+    avg = 8
+    say(f"needles: ctx {S}, avg_budget {avg}, bf16 centroids (scan at 2 tiles per wave)")
+    q, k, v, pos = _needle_layer(S, seed=11)
+    c = ops.centroid_build(k, BS, centroid_dtype=torch.bfloat16)
+    out, table, lens = ops.decode_fused(q, k, v, c, BS, ops.BudgetParams(avg_budget=avg),
+                                        append_new=1, return_selection=True)
+    torch.cuda.synchronize()
+    table, lens = table[0].cpu().numpy(), lens[0].cpu().numpy()
+    q_np = q[0].float().cpu().numpy()
+    _oracle_check(q_np, c[0].float().cpu().numpy(), table, lens, avg)
+    assert abs(lens.mean() - avg) <= 1.0
+    _check_output(out[0].float().cpu().numpy(), _ref_selected(q_np, k[0], v[0], table, lens, S))
+
+
 def test_config2_32k_half_peaked():
     ops = _ops()
     S, avg = 32768, 8
@@ -140,13 +160,14 @@ def test_config2_32k_half_peaked():
     _check_output(out[0].float().cpu().numpy(), _ref_selected(q_np, k[0], v[0], table, lens, S))
 
 
-def test_config4_ragged_batch():
+@pytest.mark.parametrize("cdt", [torch.float32, torch.bfloat16])
+def test_config4_ragged_batch(cdt):
     ops = _ops()
     B, avg = 8, 16
     rng = np.random.RandomState(4)
     lens_tok = rng.randint(16384, 131072 + 1, size=B).astype(np.int32)
     S = int(lens_tok.max())
-    say(f"config 4: ragged batch of {B}, lengths {lens_tok.tolist()}, avg_budget {avg}")
+    say(f"config 4: ragged batch of {B}, lengths {lens_tok.tolist()}, avg_budget {avg}, centroids {cdt}")
     gen = torch.Generator(device=DEV).manual_seed(4)
     q = torch.randn(B, HQ, D, device=DEV, generator=gen).to(torch.bfloat16)
     k = torch.empty(B, HKV, S, D, device=DEV, dtype=torch.bfloat16)
@@ -157,7 +178,7 @@ def test_config4_ragged_batch():
         k[b] = kb.to(torch.bfloat16)
         v[b] = torch.randn(HKV, S, D, device=DEV, generator=gen).to(torch.bfloat16)
     sl = torch.from_numpy(lens_tok).to(DEV)
-    c = ops.centroid_build(k, BS, seq_lens=sl, centroid_dtype=torch.float32)
+    c = ops.centroid_build(k, BS, seq_lens=sl, centroid_dtype=cdt)
     out, table, lens = ops.decode_fused(q, k, v, c, BS, ops.BudgetParams(avg_budget=avg), seq_lens=sl,
                                         return_selection=True)
     torch.cuda.synchronize()
