@@ -486,8 +486,15 @@ void launch_score_g(const ScoreArgs& a, dim3 grid, hipStream_t s) {
 // would hold fewer than kScoreFill workgroups (short contexts: more, shorter
 // waves, and finer sub-chunk maxima for the selection's threshold), as long as
 // the records still fit their pitch.
+// Rows any sequence can have: every length is clamped to uniform_len on the
+// device, so a summary buffer allocated for more blocks is not scanned past it.
+inline int score_rows(const ScoreArgs& a) {
+  return std::min(a.max_blocks, (a.uniform_len + a.bs - 1) / a.bs);
+}
+
 inline int score_tiles(const ScoreArgs& a) {
-  auto chunks = [&](int tpw) { return (a.max_blocks + 64 * tpw - 1) / (64 * tpw); };
+  const int rows = score_rows(a);
+  auto chunks = [&](int tpw) { return (rows + 64 * tpw - 1) / (64 * tpw); };
   int tpw = kScoreTiles;
   while (tpw > 1 && (int64_t)chunks(tpw) * a.Hkv * a.B < kScoreFill &&
          (a.parts == nullptr || chunks(tpw / 2) <= a.parts_pitch))
@@ -505,7 +512,7 @@ hipError_t launch_score_d(ScoreArgs& a, hipStream_t s) {
     tpw = score_tiles(a);
     a.chunk_rows = 4 * 16 * tpw;                                // 4 waves of 16-row tiles per record
   }
-  a.n_chunks = (a.max_blocks + a.chunk_rows - 1) / a.chunk_rows;
+  a.n_chunks = (score_rows(a) + a.chunk_rows - 1) / a.chunk_rows;
   // blocks holding the newest n_new tokens: at most ceil(n_new / bs) + 1
   a.n_app = a.n_new > 0 ? std::min((a.n_new + a.bs - 1) / a.bs + 1, a.max_blocks) : 0;
   dim3 grid((unsigned)((int64_t)(a.n_app + a.n_chunks) * a.Hkv * a.B));
