@@ -174,6 +174,13 @@ CentroidArgs centroid_args(const adakv_geometry_t* g, const adakv_kv_t* kv, cons
   return a;
 }
 
+// Blocks any sequence can have: lengths are clamped to max_seq_len on the
+// device, so the selection kernels' shapes (scores per thread, the fused
+// kernel's eligibility) follow this bound, not the summary buffer's capacity.
+int rows_bound(const adakv_geometry_t* g) {
+  return std::min(g->max_blocks, (g->max_seq_len + g->block_size - 1) / g->block_size);
+}
+
 ScoreArgs score_args(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_centroid_t* c,
                      const int32_t* lens, float* scores, int sp) {
   ScoreArgs sa{};
@@ -229,9 +236,9 @@ int run_plan(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_cent
   SelectArgs se;
   int st;
   if ((st = run_scores(g, q, c, kv_append, n_new, lens, p, table, T, ws, s, &se))) return st;
-  if (p->policy == ADAKV_POLICY_NUCLEUS && launch_nucleus(se, g->max_blocks, s) != hipSuccess)
+  if (p->policy == ADAKV_POLICY_NUCLEUS && launch_nucleus(se, rows_bound(g), s) != hipSuccess)
     return ADAKV_ERR_LAUNCH;
-  if (launch_select(se, g->max_blocks, s) != hipSuccess) return ADAKV_ERR_LAUNCH;
+  if (launch_select(se, rows_bound(g), s) != hipSuccess) return ADAKV_ERR_LAUNCH;
   if (!sel_lens) return ADAKV_OK;
   BudgetArgs ba{};
   ba.wbuf = se.wbuf;
@@ -470,15 +477,15 @@ int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const 
   // decode of every head (the nucleus policy adds its weight kernel in between)
   if (kv->dtype != ADAKV_F32 && q->dtype == kv->dtype && aligned16(q->data) && q->stride_b % 8 == 0 &&
       q->stride_h % 8 == 0 &&
-      select_decode_supported(g->head_dim, g->max_blocks, T, g->n_q_heads, L.sp, L.parts_pitch) &&
-      select_decode_lds(g->head_dim, g->n_q_heads, g->max_blocks) <= max_lds_per_block()) {
+      select_decode_supported(g->head_dim, rows_bound(g), T, g->n_q_heads, L.sp, L.parts_pitch) &&
+      select_decode_lds(g->head_dim, g->n_q_heads, rows_bound(g)) <= max_lds_per_block()) {
     FusedArgs fa{};
     if ((st = run_scores(g, q, c, kv, append_new, seq_lens, p, table, Tl, w, s, &fa.s))) return st;
-    if (p->policy == ADAKV_POLICY_NUCLEUS && launch_nucleus(fa.s, g->max_blocks, s) != hipSuccess)
+    if (p->policy == ADAKV_POLICY_NUCLEUS && launch_nucleus(fa.s, rows_bound(g), s) != hipSuccess)
       return ADAKV_ERR_LAUNCH;
     fa.d = decode_args(g, q, kv, seq_lens, sm_scale, out);
     fa.d.sel_lens_out = lens;
-    return status_of(launch_select_decode(fa, kv->dtype, g->head_dim, g->max_blocks, s));
+    return status_of(launch_select_decode(fa, kv->dtype, g->head_dim, rows_bound(g), s));
   }
   if ((st = run_plan(g, q, c, kv, append_new, seq_lens, p, table, Tl, nullptr, w, s))) return st;
   // the selection kernel lists distinct valid blocks: no union needed per head

@@ -192,18 +192,20 @@ def test_config4_ragged_batch(cdt):
         _check_output(out[b].float().cpu().numpy(), _ref_selected(q_np, k[b], v[b], table[b], lens[b], Sb))
 
 
+@pytest.mark.parametrize("cap", [131072, 262144])
 @pytest.mark.parametrize("cdt", [torch.float32, torch.bfloat16])
-def test_overallocated_summaries_match_tight(cdt):
-    """A summary buffer allocated for 131072 tokens while K holds 20000: the
-    scan is sized by the length bound (not the buffer), so the step's
+def test_overallocated_summaries_match_tight(cdt, cap):
+    """A summary buffer allocated for 128K / 256K tokens while K holds 20000:
+    the scan and the selection kernels are shaped by the length bound (not the
+    buffer; a 16384-block buffer stays on the fused path), so the step's
     selection and output are bit-identical to those over a tight buffer."""
     ops = _ops()
     S, avg = 20000, 8
-    say(f"over-allocated summaries: ctx {S} in a buffer of 8192 blocks, centroids {cdt}")
+    say(f"over-allocated summaries: ctx {S} in a buffer of {cap // BS} blocks, centroids {cdt}")
     q, k, v, _ = _needle_layer(S, seed=13)
     tight = ops.centroid_build(k, BS, centroid_dtype=cdt)
-    wide = ops.centroid_build(k, BS, centroid_dtype=cdt, max_blocks=131072 // BS)
-    assert wide.shape[2] == 8192 and tight.shape[2] == -(-S // BS)
+    wide = ops.centroid_build(k, BS, centroid_dtype=cdt, max_blocks=cap // BS)
+    assert wide.shape[2] == cap // BS and tight.shape[2] == -(-S // BS)
     p = ops.BudgetParams(avg_budget=avg)
     o1, t1, l1 = ops.decode_fused(q, k, v, tight, BS, p, return_selection=True)
     o2, t2, l2 = ops.decode_fused(q, k, v, wide, BS, p, return_selection=True)
