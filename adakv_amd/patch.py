@@ -286,6 +286,11 @@ def adakv_attention_forward(module, query, key, value, attention_mask, scaling, 
     want = instrumentation_active()
     budget = _budget(cfg)
     if not any(starts):
+        # a view of the tokens any row holds: a static cache larger than the
+        # context is then scanned and selected over that context only
+        n = max(max(lens), 1)
+        if n < S:
+            key, value = key[:, :, :n], value[:, :, :n]
         res = [ops.decode_fused(query[:, :, 0, :], key, value, st.centroid, bs, budget, seq_lens=lens_dev,
                                 append_new=append_new, sm_scale=scaling, out=out[:, 0],
                                 return_selection=want, estimator=cfg["estimator"])]
