@@ -132,6 +132,14 @@ __device__ __forceinline__ uint4 load16(const void* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
+// A 16-byte load of data read once (a streaming scan): non-temporal, so it
+// does not displace what the caches hold for later kernels.
+__device__ __forceinline__ uint4 load16_stream(const void* p) {
+  typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 // ---- cross-lane data movement --------------------------------------------------
 // DPP moves (full-rate VALU, no LDS traffic).  Controls: quad_perm [1,0,3,2] = 0xB1,
 // quad_perm [2,3,0,1] = 0x4E, row_half_mirror = 0x141, row_mirror = 0x140.

@@ -43,6 +43,7 @@ struct ScoreArgs {
   int parts_pitch;
   BudgetCfg cfg;
   int n_app, n_chunks, chunk_rows;   // set by the launcher
+  int stream_loads;                  // set by the launcher: non-temporal summary loads
   int q_vec;                   // 1: q has the summary type and 16-byte aligned rows (vector loads)
   int minmax;                  // 1: rows are minmax summaries [max | min] of 2*head_dim elements
 };
