@@ -88,6 +88,67 @@ def test_nucleus_counts_match_oracle_on_gpu_scores(P, T, scale, nb_tokens):
     say(f"  {excl} heads excluded")
 
 
+@pytest.mark.parametrize("P", [0.95])
+def test_nucleus_crossing_in_the_tail_bin(P):
+    """One dominant block per KV head and 8191 blocks more than 255/16 octaves
+    of probability below it: for most heads the crossing of P falls in the
+    radix search's last (tail) bin, so the weight kernel takes its four extra
+    passes over all 31 bits of the distance.  Centroids are set directly
+    (score = q[0] * c[0]).  Counts are held to the oracle's on the GPU's own
+    scores wherever NumPy's fp32 running sum fixes them; a tail crossing sums
+    about 10^3 terms of 1e-5, inside that sum's error, so those heads' counts
+    are checked only against the budget bounds (their exact value is not
+    pinned here)."""
+    ops = _ops()
+    Hq, Hkv, D, bs, S = 32, 8, 64, 16, 131072
+    G = Hq // Hkv
+    nb = S // bs
+    say(f"nucleus tail crossing P={P}, {nb} blocks")
+    rng = np.random.RandomState(int(P * 1000))
+    C = np.zeros((1, Hkv, nb, D), np.float32)
+    for g in range(Hkv):
+        C[0, g, :, 0] = (-11.3 - 0.05 * g + rng.uniform(-0.15, 0.15, nb)).astype(np.float32)
+        C[0, g, 100 + 7 * g, 0] = 0.0
+    q = np.zeros((1, Hq, D), np.float32)
+    for h in range(Hq):
+        q[0, h, 0] = np.float32(1.0 + 0.02 * (h % G))
+    c = torch.from_numpy(C).to(DEV)
+    qt = torch.from_numpy(q).to(DEV)
+    p = dict(avg=12, kmin=2, kmax=256, sink=1, local=4, cmin=1, temp=1.0, nucleus_p=P)
+    sc = ops.block_scores(qt, c, bs, seq_len=S)
+    table, lens = ops.plan(qt, c, bs, _budget(ops, p), seq_len=S)
+    torch.cuda.synchronize()
+    scores = sc[0, :, :nb].cpu().numpy()
+    # the branch is reached: the crossing block lies more than 255/16 octaves below the maximum
+    z = scores.astype(np.float64) - scores.max(axis=1, keepdims=True)
+    pr = np.sort(np.exp(z) / np.exp(z).sum(axis=1, keepdims=True), axis=1)[:, ::-1]
+    kstar = (np.cumsum(pr, axis=1) < P).sum(axis=1)
+    deep = np.log2(pr[np.arange(Hq), kstar] / pr[:, 0]) < -255.0 / 16
+    say(f"  {int(deep.sum())}/{Hq} heads cross P in the tail bin")
+    assert deep.sum() >= 8
+    lo, _, target, _ = O.budget_bounds(nb, p["avg"], p["kmin"], p["kmax"], p["sink"], p["local"], p["cmin"])
+    amb, margin = nucleus_exclusions(scores, lo, target, 1.0, P)
+    k_or = O.allocate_budget(scores, p["avg"], min(p["kmin"], nb), min(p["kmax"], nb), temperature=1.0,
+                             policy="adaptive_nucleus", nucleus_p=P,
+                             floor=min(p["sink"], nb) + min(p["local"], nb) + p["cmin"])
+    w = O.budget_weights(scores, "adaptive_nucleus", 1.0, P)
+    say(f"  nucleus weights {int(w.min())} .. {int(w.max())}, {int(amb.sum())} knife-edge heads")
+    # the 8191 low scores lie within 0.4 of each other, so most heads' selections
+    # end on a score near-tie; what this case pins is the counts, compared on
+    # every head whose budget is not at a rounding knife-edge
+    excl = compare_selection(scores, table[0].cpu().numpy(), lens[0].cpu().numpy(), k_oracle=k_or,
+                             w_oracle=w, lo=lo, target=target, sink=p["sink"], local=p["local"],
+                             cmin=p["cmin"], policy="adaptive_nucleus", exclude=amb, half_margin=margin,
+                             max_excluded=1.0)
+    counted = ~(O.budget_near_half(w, lo, target, margin=margin) | amb)
+    say(f"  counts compared on {int(counted.sum())} heads ({int((counted & deep).sum())} crossing in the tail), "
+        f"{excl} heads excluded from the selection comparison")
+    assert counted.sum() >= 8
+    k = lens[0].cpu().numpy()
+    floor = min(p["sink"], nb) + min(p["local"], nb) + p["cmin"]
+    assert np.all(k >= max(lo, floor)) and np.all(k <= max(min(p["kmax"], nb), floor))
+
+
 def test_nucleus_plan_matches_reference_golden():
     """fp32 path vs the reference's own mask and counts (golden nucleus case)."""
     ops = _ops()
