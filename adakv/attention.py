@@ -17,7 +17,7 @@ import math
 
 import torch
 
-from . import ops
+from adakv_amd import ops
 
 # --- realised-budget instrumentation (adakv/attention.py:24-45) -------------
 _BUDGET_TRACE = None

@@ -27,8 +27,8 @@ import math
 
 import torch
 
-from . import _capi as C
-from .ops import _dt, _on_device, _ptr, _stream
+from adakv_amd import _capi as C
+from adakv_amd.ops import _dt, _on_device, _ptr, _stream
 
 __all__ = [
     "expand_kv_heads",

@@ -15,7 +15,7 @@ Output:
 """
 from __future__ import annotations
 
-from .. import _capi, ops
+from adakv_amd import _capi, ops
 
 #: True when the HIP library is built and a ROCm device is visible.
 HAS_HIP = False

@@ -1,7 +1,7 @@
 """Plug AdaKV into a HuggingFace model through the attention interface
 (adakv/patch.py; transformers >= 5).
 
-    from adakv_amd.patch import patch_model
+    from adakv.patch import patch_model
     patch_model(model, block_size=16, avg_budget=8)   # install + enable
     ... model.generate(...) ...
     disable_adakv()
@@ -41,7 +41,7 @@ from __future__ import annotations
 import torch
 
 from . import baselines_rt as _brt
-from . import ops
+from adakv_amd import ops
 from .attention import instrumentation_active, record_selection
 
 try:

@@ -1,9 +1,10 @@
-"""AdaKV decode hot path for AMD Instinct MI355X (gfx950).
+"""Native AdaKV decode library for AMD Instinct MI355X (gfx950).
 
-Query-aware, per-head-adaptive block-sparse decode attention: centroid block
-scores, an entropy-driven per-head budget, top-k block selection and a ragged
-split-K flash-decode, all as HIP kernels behind the C ABI in
-``include/adakv_amd.h``.  The Python modules mirror the reference package's
-API (``patch``, ``attention``, ``runtime``, ``kernels.block_sparse_decode``).
+``csrc/`` holds the HIP kernels and the C ABI of ``include/adakv_amd.h``
+(centroid build and append, block scores, budget, selection, sparse and dense
+flash-decode, the fused decode step, the eviction baselines), built in-tree
+into ``_lib/libadakv_amd.so`` by ``adakv_amd.build``.  ``_capi`` binds it with
+ctypes and ``ops`` wraps it for torch tensors.  The reference's Python API
+(``adakv.patch``, ``adakv.attention``, ...) lives in the package ``adakv``.
 """
-__version__ = "0.1.0"
+__version__ = "0.2.0"

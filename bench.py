@@ -347,7 +347,7 @@ def evict_bench(torch, ops, w, stream, seed, h2o_len):
     headline 128K context) against the matrix-core and HBM rooflines and
     against the reference's torch formulation, the retention, and the frozen
     decode step on the headline workload."""
-    from adakv_amd import baselines_rt as BR
+    from adakv import baselines_rt as BR
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
@@ -423,7 +423,7 @@ def model_step(args):
     from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, sdpa_mask
 
     from adakv_amd import ops
-    from adakv_amd import patch as P
+    from adakv import patch as P
     dev = torch.device("cuda:0")
     L, B, S0 = args.model_layers, args.model_batch, args.model_ctx
     cfg = LlamaConfig(vocab_size=128256, hidden_size=8192, intermediate_size=28672, num_hidden_layers=L,

@@ -187,8 +187,8 @@ def test_python_errors_mirror_the_reference(lib):
     (the reference raises RuntimeError without its GPU kernel)."""
     import torch
 
-    from adakv_amd.attention import AdaKVCache, plan_selection
-    from adakv_amd.kernels.block_sparse_decode import block_sparse_decode
+    from adakv.attention import AdaKVCache, plan_selection
+    from adakv.kernels.block_sparse_decode import block_sparse_decode
     with pytest.raises(ValueError):
         AdaKVCache(16, estimator="bogus")
     cache = AdaKVCache(16)

@@ -44,7 +44,7 @@ def _gpu():
 
 
 def _BR():
-    from adakv_amd import baselines_rt
+    from adakv import baselines_rt
     return baselines_rt
 
 

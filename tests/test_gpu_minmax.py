@@ -257,7 +257,7 @@ def test_minmax_cache_and_factorial_cells():
     (estimator, policy) cell runs, keeps >= c_min content blocks per head,
     honours a fixed budget and agrees with the oracle's mask
     (tests/test_factorial_selection.py:42-108)."""
-    from adakv_amd.attention import AdaKVCache, plan_selection
+    from adakv.attention import AdaKVCache, plan_selection
     say("minmax cache + factorial cells")
     q, k, v = _factorial_fixture()
     cc = AdaKVCache(16, "centroid").append_prefill(k, v)
@@ -296,7 +296,7 @@ def test_minmax_cache_and_factorial_cells():
 def test_minmax_cache_decode_append_and_attention():
     """append_decode refreshes the bounds (equal to a rebuild) and a decode
     step with estimator="minmax" attends over exactly its own selection."""
-    from adakv_amd import attention as A
+    from adakv import attention as A
     say("minmax cache append_decode + adakv_decode_attention")
     rng = np.random.RandomState(7)
     Hkv, S, D, G = 4, 2000, 128, 4

@@ -240,7 +240,7 @@ def test_all_six_factorial_cells_match_the_oracle():
     """tests/test_factorial_selection.py:42-108 with every policy built:
     all cells run, keep >= c_min content blocks, fixed honours its budget,
     adaptive policies land near the target mean, masks agree with the oracle."""
-    from adakv_amd.attention import AdaKVCache, plan_selection
+    from adakv.attention import AdaKVCache, plan_selection
     say("factorial cells incl. adaptive_nucleus")
     rng = np.random.RandomState(0)
     k = torch.from_numpy(rng.standard_normal((2, 320, 64)).astype(np.float32)).to(DEV)

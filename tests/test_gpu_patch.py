@@ -36,7 +36,7 @@ def _gpu():
 
 def _model(dtype):
     from transformers import LlamaConfig, LlamaForCausalLM
-    from adakv_amd.patch import install_adakv
+    from adakv.patch import install_adakv
     cfg = LlamaConfig(vocab_size=VOCAB, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
                       num_attention_heads=8, num_key_value_heads=2, head_dim=64,
                       max_position_embeddings=4096)
@@ -80,8 +80,8 @@ def _decode_logits(model, ids, cache_kind, attention_mask=None):
 
 def _run(model, ids, cache_kind, cfg, attention_mask=None):
     """(patched logits, unpatched logits, layer-steps recorded by the HIP path)."""
-    from adakv_amd import attention as A
-    from adakv_amd.patch import disable_adakv, enable_adakv
+    from adakv import attention as A
+    from adakv.patch import disable_adakv, enable_adakv
     disable_adakv()
     ref = _decode_logits(model, ids, cache_kind, attention_mask)
     enable_adakv(**cfg)
@@ -177,8 +177,8 @@ def test_generate_with_static_cache_matches_sdpa_greedy():
     with a budget that selects every block the greedy continuation equals the
     unpatched model's, and every decode step ran on the HIP path."""
     from transformers import StaticCache
-    from adakv_amd import attention as A
-    from adakv_amd.patch import disable_adakv, enable_adakv
+    from adakv import attention as A
+    from adakv.patch import disable_adakv, enable_adakv
     say("patch generate() with StaticCache, fp32, full budget")
     model = _model(torch.float32)
     ids = _ids(2)

@@ -1,5 +1,5 @@
 """Host logic of the HuggingFace hook on the CPU: reading per-sequence runs
-from HF's decode masks (adakv_amd.patch._mask_runs), which decides between the
+from HF's decode masks (adakv.patch._mask_runs), which decides between the
 batched sparse path, the per-sequence path and SDPA, and the mask function
 registered for the "adakv" attention implementation."""
 from __future__ import annotations
@@ -9,7 +9,7 @@ import pytest
 torch = pytest.importorskip("torch")
 pytest.importorskip("transformers")
 
-from adakv_amd import patch as P  # noqa: E402
+from adakv import patch as P  # noqa: E402
 
 
 def _mask(rows, kv_len, additive=False):
