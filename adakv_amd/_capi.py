@@ -23,11 +23,13 @@ ADAKV_ERR_UNSUPPORTED = 4
 ADAKV_ERR_WORKSPACE = 5
 ADAKV_ERR_LAUNCH = 6
 ADAKV_ERR_VALUE = 7
+ADAKV_ERR_SCRATCH = 8
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 ADAKV_F32, ADAKV_F16, ADAKV_BF16 = 0, 1, 2
 POLICY_FIXED, POLICY_ADAPTIVE, POLICY_NUCLEUS = 0, 1, 2
 SUMMARY_CENTROID, SUMMARY_MINMAX = 0, 1
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class Geometry(ctypes.Structure):
@@ -91,6 +93,9 @@ SIGNATURES = {
     "adakv_decode_fused": (ctypes.c_int, [P(Geometry), P(Query), P(KV), P(Centroid), c_void_p,
                                           P(Budget), P(Selection), c_int32, ctypes.c_float,
                                           P(Output), c_void_p, ctypes.c_size_t, c_void_p]),
+    "adakv_decode_fused_noalloc": (ctypes.c_int, [P(Geometry), P(Query), P(KV), P(Centroid), c_void_p,
+                                                  P(Budget), P(Selection), c_int32, ctypes.c_float,
+                                                  P(Output), c_void_p]),
     "adakv_dense_decode": (ctypes.c_int, [P(Geometry), P(Query), P(KV), c_void_p, ctypes.c_float,
                                           P(Output), c_void_p, ctypes.c_size_t, c_void_p]),
     "adakv_importance_workspace_bytes": (ctypes.c_size_t, [P(Prompt), c_int32]),
@@ -153,7 +158,7 @@ def check(status: int, what: str) -> None:
     if status == ADAKV_OK:
         return
     msg = f"{what}: {load().adakv_status_string(status).decode()} (status {status})"
-    if status in (ADAKV_ERR_NULL, ADAKV_ERR_SHAPE, ADAKV_ERR_DTYPE, ADAKV_ERR_VALUE,
+    if status in (ADAKV_ERR_NULL, ADAKV_ERR_SHAPE, ADAKV_ERR_DTYPE, ADAKV_ERR_VALUE, ADAKV_ERR_SCRATCH,
                   ADAKV_ERR_UNSUPPORTED):
         raise ValueError(msg)
     raise AdaKVError(msg)

@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "adakv_amd.h"
 #include "internal.hpp"
@@ -357,6 +358,109 @@ WorkspaceLayout workspace_layout(const adakv_geometry_t& g, int T) {
 
 }  // namespace adakv
 
+// ---- static scratch of adakv_decode_fused_noalloc ---------------------------
+// The workspace of the allocation-free entry point: a file-scope device array,
+// one copy per GPU, held until the process ends.  Host code never passes the
+// array's name to a kernel (in host code it is a host-side stand-in); it uses
+// the per-device address from hipGetSymbolAddress, looked up once per device.
+static __device__ __align__(256) unsigned char scratch[ADAKV_NOALLOC_SCRATCH_BYTES];
+
+namespace adakv {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// The device address of `scratch` on the stream's device.  The first call on a
+// device looks it up (that device current) and clears the hand-off counters at
+// its front with a fill kernel on the stream (every call leaves them zero).
+int static_scratch(hipStream_t s, void** out) {
+  int dev = -1;
+  if (s == nullptr || hipStreamGetDevice(s, &dev) != hipSuccess) {
+    if (hipGetDevice(&dev) != hipSuccess) return ADAKV_ERR_LAUNCH;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return ADAKV_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return ADAKV_ERR_LAUNCH;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return ADAKV_ERR_LAUNCH;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess && p != nullptr) {
+      hipLaunchKernelGGL(zero_words_kernel, dim3(16), dim3(256), 0, s, reinterpret_cast<uint32_t*>(p),
+                         (int)(kCounterBytes / 4));
+    }
+    const hipError_t e2 = hipGetLastError();
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || p == nullptr || e2 != hipSuccess) return ADAKV_ERR_LAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ADAKV_OK;
+}
+
+int decode_fused_impl(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
+                       const adakv_centroid_t* c, const int32_t* seq_lens,
+                       const adakv_budget_t* p, const adakv_selection_t* sel, int32_t append_new,
+                       float sm_scale, const adakv_output_t* out, void* ws, size_t ws_bytes,
+                       void* stream, bool static_ws) {
+  int st;
+  if ((st = check_geometry(g)) || (st = check_q(q)) || (st = check_kv(g, kv, true)) ||
+      (st = check_centroid(g, c)) || (st = check_budget(p)) || (st = check_out(out)))
+    return st;
+  if (append_new < 0 || append_new > g->max_seq_len) return ADAKV_ERR_VALUE;
+  if (!isfinite(sm_scale)) return ADAKV_ERR_VALUE;
+  const int T = table_width_of(g, p);
+  int Tl = T;
+  if (sel) {
+    if (!sel->block_table || !sel->sel_lens) return ADAKV_ERR_NULL;
+    if (sel->table_width < T) return ADAKV_ERR_SHAPE;
+    Tl = sel->table_width;
+  }
+  if (static_ws) {
+    // every argument is checked before the scratch is looked up (the first
+    // call on a device launches its counter fill)
+    if (append_new > 0 && !centroid_pair_ok(kv->dtype, c)) return ADAKV_ERR_DTYPE;
+    if (workspace_layout(*g, Tl).total > ADAKV_NOALLOC_SCRATCH_BYTES) return ADAKV_ERR_SCRATCH;
+    if ((st = static_scratch((hipStream_t)stream, &ws))) return st;
+  } else if ((st = check_ws(g, Tl, ws, ws_bytes))) {
+    return st;
+  }
+  char* w = reinterpret_cast<char*>(ws);
+  const WorkspaceLayout L = workspace_layout(*g, Tl);
+  int32_t* table = sel ? sel->block_table : reinterpret_cast<int32_t*>(w + L.table);
+  int32_t* lens = sel ? sel->sel_lens : reinterpret_cast<int32_t*>(w + L.lens);
+  const hipStream_t s = (hipStream_t)stream;
+  if (append_new > 0 && !centroid_pair_ok(kv->dtype, c)) return ADAKV_ERR_DTYPE;
+  // bf16 / fp16 K/V (and q of the same type, 16-byte aligned rows) on a shape the fused kernel
+  // serves: scores, then one kernel for the budget, the selection and the
+  // decode of every head (the nucleus policy adds its weight kernel in between)
+  if (kv->dtype != ADAKV_F32 && q->dtype == kv->dtype && aligned16(q->data) && q->stride_b % 8 == 0 &&
+      q->stride_h % 8 == 0 &&
+      select_decode_supported(g->head_dim, rows_bound(g), T, g->n_q_heads, L.sp, L.parts_pitch) &&
+      select_decode_lds(g->head_dim, g->n_q_heads, rows_bound(g)) <= max_lds_per_block()) {
+    FusedArgs fa{};
+    if ((st = run_scores(g, q, c, kv, append_new, seq_lens, p, table, Tl, w, s, &fa.s))) return st;
+    if (p->policy == ADAKV_POLICY_NUCLEUS && launch_nucleus(fa.s, rows_bound(g), s) != hipSuccess)
+      return ADAKV_ERR_LAUNCH;
+    fa.d = decode_args(g, q, kv, seq_lens, sm_scale, out);
+    fa.d.sel_lens_out = lens;
+    return status_of(launch_select_decode(fa, kv->dtype, g->head_dim, rows_bound(g), s));
+  }
+  if ((st = run_plan(g, q, c, kv, append_new, seq_lens, p, table, Tl, nullptr, w, s))) return st;
+  // the selection kernel lists distinct valid blocks: no union needed per head
+  return run_decode(g, q, kv, seq_lens, table, Tl, nullptr, p, lens, sm_scale, out, w, Tl, true, s);
+}
+
+}  // namespace
+}  // namespace adakv
+
 using namespace adakv;
 
 extern "C" {
@@ -371,6 +475,7 @@ const char* adakv_status_string(int status) {
     case ADAKV_ERR_WORKSPACE: return "workspace too small or misaligned";
     case ADAKV_ERR_LAUNCH: return "HIP kernel launch failed";
     case ADAKV_ERR_VALUE: return "invalid parameter value or alignment";
+    case ADAKV_ERR_SCRATCH: return "the step needs more scratch than ADAKV_NOALLOC_SCRATCH_BYTES";
     default: return "unknown status";
   }
 }
@@ -452,44 +557,16 @@ int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const 
                        const adakv_budget_t* p, const adakv_selection_t* sel, int32_t append_new,
                        float sm_scale, const adakv_output_t* out, void* ws, size_t ws_bytes,
                        void* stream) {
-  int st;
-  if ((st = check_geometry(g)) || (st = check_q(q)) || (st = check_kv(g, kv, true)) ||
-      (st = check_centroid(g, c)) || (st = check_budget(p)) || (st = check_out(out)))
-    return st;
-  if (append_new < 0 || append_new > g->max_seq_len) return ADAKV_ERR_VALUE;
-  if (!isfinite(sm_scale)) return ADAKV_ERR_VALUE;
-  const int T = table_width_of(g, p);
-  int Tl = T;
-  if (sel) {
-    if (!sel->block_table || !sel->sel_lens) return ADAKV_ERR_NULL;
-    if (sel->table_width < T) return ADAKV_ERR_SHAPE;
-    Tl = sel->table_width;
-  }
-  if ((st = check_ws(g, Tl, ws, ws_bytes))) return st;
-  char* w = reinterpret_cast<char*>(ws);
-  const WorkspaceLayout L = workspace_layout(*g, Tl);
-  int32_t* table = sel ? sel->block_table : reinterpret_cast<int32_t*>(w + L.table);
-  int32_t* lens = sel ? sel->sel_lens : reinterpret_cast<int32_t*>(w + L.lens);
-  const hipStream_t s = (hipStream_t)stream;
-  if (append_new > 0 && !centroid_pair_ok(kv->dtype, c)) return ADAKV_ERR_DTYPE;
-  // bf16 / fp16 K/V (and q of the same type, 16-byte aligned rows) on a shape the fused kernel
-  // serves: scores, then one kernel for the budget, the selection and the
-  // decode of every head (the nucleus policy adds its weight kernel in between)
-  if (kv->dtype != ADAKV_F32 && q->dtype == kv->dtype && aligned16(q->data) && q->stride_b % 8 == 0 &&
-      q->stride_h % 8 == 0 &&
-      select_decode_supported(g->head_dim, rows_bound(g), T, g->n_q_heads, L.sp, L.parts_pitch) &&
-      select_decode_lds(g->head_dim, g->n_q_heads, rows_bound(g)) <= max_lds_per_block()) {
-    FusedArgs fa{};
-    if ((st = run_scores(g, q, c, kv, append_new, seq_lens, p, table, Tl, w, s, &fa.s))) return st;
-    if (p->policy == ADAKV_POLICY_NUCLEUS && launch_nucleus(fa.s, rows_bound(g), s) != hipSuccess)
-      return ADAKV_ERR_LAUNCH;
-    fa.d = decode_args(g, q, kv, seq_lens, sm_scale, out);
-    fa.d.sel_lens_out = lens;
-    return status_of(launch_select_decode(fa, kv->dtype, g->head_dim, rows_bound(g), s));
-  }
-  if ((st = run_plan(g, q, c, kv, append_new, seq_lens, p, table, Tl, nullptr, w, s))) return st;
-  // the selection kernel lists distinct valid blocks: no union needed per head
-  return run_decode(g, q, kv, seq_lens, table, Tl, nullptr, p, lens, sm_scale, out, w, Tl, true, s);
+  return decode_fused_impl(g, q, kv, c, seq_lens, p, sel, append_new, sm_scale, out, ws, ws_bytes, stream,
+                           false);
+}
+
+int adakv_decode_fused_noalloc(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
+                               const adakv_centroid_t* c, const int32_t* seq_lens,
+                               const adakv_budget_t* p, const adakv_selection_t* sel, int32_t append_new,
+                               float sm_scale, const adakv_output_t* out, void* stream) {
+  return decode_fused_impl(g, q, kv, c, seq_lens, p, sel, append_new, sm_scale, out, nullptr,
+                           ADAKV_NOALLOC_SCRATCH_BYTES, stream, true);
 }
 
 int adakv_dense_decode(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,

@@ -55,7 +55,7 @@
 extern "C" {
 #endif
 
-#define ADAKV_ABI_VERSION 4
+#define ADAKV_ABI_VERSION 5
 
 /* Status codes.  Argument errors are detected on the host before any launch. */
 enum {
@@ -66,8 +66,16 @@ enum {
   ADAKV_ERR_UNSUPPORTED = 4,  /* valid but not built: head_dim, group, max_blocks  */
   ADAKV_ERR_WORKSPACE = 5,    /* workspace too small or not 256-byte aligned       */
   ADAKV_ERR_LAUNCH = 6,       /* the HIP runtime reported a launch error           */
-  ADAKV_ERR_VALUE = 7         /* bad parameter value (budget, policy, alignment)   */
+  ADAKV_ERR_VALUE = 7,        /* bad parameter value (budget, policy, alignment)   */
+  ADAKV_ERR_SCRATCH = 8       /* the step needs more scratch than the static array
+                               * of adakv_decode_fused_noalloc holds                */
 };
+
+/* Bytes of the static device scratch array behind adakv_decode_fused_noalloc
+ * (one per GPU, held by the library until the process ends).  It covers, at
+ * block_size 16 and head_dim 128: batch 1 up to 512K tokens (32 q / 8 KV
+ * heads), batch 8 at 128K, batch 4 with 64 q heads at 64K. */
+#define ADAKV_NOALLOC_SCRATCH_BYTES (16u << 20)
 
 enum { ADAKV_F32 = 0, ADAKV_F16 = 1, ADAKV_BF16 = 2 };
 
@@ -190,6 +198,23 @@ int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const 
                        const adakv_budget_t* budget, const adakv_selection_t* sel,
                        int32_t append_new, float sm_scale, const adakv_output_t* out,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* adakv_decode_fused without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops or
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * scratch is a static device array of ADAKV_NOALLOC_SCRATCH_BYTES inside the
+ * library, one per GPU, shared by every call on that GPU: calls that overlap
+ * on one GPU (different streams or host threads) race and must not be issued;
+ * calls ordered on one stream are safe.  A geometry whose workspace
+ * (adakv_workspace_bytes) exceeds the array returns ADAKV_ERR_SCRATCH before
+ * any launch.  The first call on a GPU looks up the array's device address
+ * and clears its hand-off counters with a fill kernel on the stream; no call
+ * allocates, frees or memsets memory. */
+int adakv_decode_fused_noalloc(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
+                               const adakv_centroid_t* centroid, const int32_t* seq_lens,
+                               const adakv_budget_t* budget, const adakv_selection_t* sel,
+                               int32_t append_new, float sm_scale, const adakv_output_t* out,
+                               void* stream);
 
 /* Dense split-K flash-decode over every token (the comparison baseline).
  * benchmarks/efficiency/bench_decode_latency.py:40-53. */

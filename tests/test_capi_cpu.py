@@ -44,8 +44,8 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_abi_version_and_status_strings(lib):
     assert lib.adakv_abi_version() == C.ABI_VERSION
-    for s in range(8):
-        assert lib.adakv_status_string(s)
+    for s in range(9):
+        assert lib.adakv_status_string(s) != b"unknown status"
     assert lib.adakv_status_string(99) == b"unknown status"
 
 
@@ -106,6 +106,32 @@ def test_null_and_dtype_validation(lib):
              ctypes.byref(out), ctypes.c_void_p(0x10010), 1 << 30, None) == C.ADAKV_ERR_WORKSPACE
     assert f(ctypes.byref(g), ctypes.byref(q), ctypes.byref(kv), None, ctypes.c_float(float("nan")),
              ctypes.byref(out), ws, 1 << 30, None) == C.ADAKV_ERR_VALUE
+
+
+def test_noalloc_refuses_a_step_larger_than_its_scratch(lib):
+    """adakv_decode_fused_noalloc checks every argument and the step's scratch
+    size on the host, before it looks up its static array or launches: here a
+    geometry of 64 sequences of 131072 tokens (whose fp32 scores alone exceed
+    ADAKV_NOALLOC_SCRATCH_BYTES) and argument errors come back on a CPU host."""
+    big = _g(B=64)
+    assert lib.adakv_workspace_bytes(ctypes.byref(big), 64) > C.NOALLOC_SCRATCH_BYTES
+    q = C.Query(0x1000, C.ADAKV_BF16, 4096, 128)
+    kv = C.KV(0x1000, 0x2000, C.ADAKV_BF16, 8 * 131072 * 128, 131072 * 128, 128)
+    c = C.Centroid(0x4000, C.ADAKV_BF16, C.SUMMARY_CENTROID)
+    out = C.Output(0x3000, C.ADAKV_BF16, 4096, 128)
+    f = lib.adakv_decode_fused_noalloc
+    bud = _b(avg_budget=8)
+    assert f(ctypes.byref(big), ctypes.byref(q), ctypes.byref(kv), ctypes.byref(c), None, ctypes.byref(bud),
+             None, 1, ctypes.c_float(0.088), ctypes.byref(out), None) == C.ADAKV_ERR_SCRATCH
+    assert b"ADAKV_NOALLOC_SCRATCH_BYTES" in lib.adakv_status_string(C.ADAKV_ERR_SCRATCH)
+    g = _g()
+    assert f(ctypes.byref(g), None, ctypes.byref(kv), ctypes.byref(c), None, ctypes.byref(bud),
+             None, 1, ctypes.c_float(0.088), ctypes.byref(out), None) == C.ADAKV_ERR_NULL
+    assert f(ctypes.byref(g), ctypes.byref(q), ctypes.byref(kv), ctypes.byref(c), None, ctypes.byref(bud),
+             None, -1, ctypes.c_float(0.088), ctypes.byref(out), None) == C.ADAKV_ERR_VALUE
+    narrow = C.Selection(0x5000, 8, 0x6000)
+    assert f(ctypes.byref(g), ctypes.byref(q), ctypes.byref(kv), ctypes.byref(c), None, ctypes.byref(bud),
+             ctypes.byref(narrow), 1, ctypes.c_float(0.088), ctypes.byref(out), None) == C.ADAKV_ERR_SHAPE
 
 
 def test_plan_validation(lib):
