@@ -1,26 +1,39 @@
-// Fused selection + sparse decode of one AdaKV decode step, after the score
-// kernel (adakv/attention.py:202-268: budget, selection and block-sparse
+// Fused budget + selection + sparse decode of one AdaKV decode step, after the
+// score kernel (adakv/attention.py:202-268: budget, selection and block-sparse
 // attention of every q-head in one launch).
 //
-// One 512-thread workgroup per (q-head, sequence) (8 waves: the matrix-core
-// decode needs more registers than a 16-wave workgroup leaves a wave):
+// One workgroup of NT threads (4 or 8 waves) per (q-head, sequence).  The step
+// is a short chain of phases with few workgroup barriers:
 //
-// 1. Loads, issued in the order they are consumed: the softmax records the
-//    score kernel left for every head of the sequence (one record per score
-//    workgroup), this head's scores, its query, and the K/V tiles of its
-//    forced sink and local blocks (known before any selection, so their HBM
-//    latency hides under the selection).
-// 2. Entropy weights of all the sequence's heads (adakv/budget.py:33-37): a
-//    16-lane row merges one head's records.  Every workgroup of the sequence
-//    evaluates the same weights in the same order, so each derives the same
-//    sum of weights in NumPy's pairwise order and its own head's count
-//    (adakv/budget.py:80-86) without any inter-workgroup hand-off.
-// 3. The top k - n_forced content blocks of this head (select.hpp), written
-//    to the block-table row and an LDS list.
+// 0. Loads, issued before anything is computed: the softmax records the score
+//    kernel left for every head of the sequence (LPH lanes per head), this
+//    head's scores (thread t owns blocks [t*IPT, (t+1)*IPT)), the query, and
+//    the K/V tiles of the head's forced sink and local blocks, which are known
+//    before any selection.
+// 1. Every head's entropy weight (adakv/budget.py:33-37) from its merged
+//    records; this thread's content maximum (an upper bound of its scores).
+//    Barrier.
+// 2. Every wave, redundantly (no barrier): the sum of weights in NumPy's
+//    pairwise order and this head's count (adakv/budget.py:80-86), KC = count
+//    - forced, and a threshold tau <= the KC-th largest thread maximum: that
+//    maximum itself for KC <= 16 (repeated wave maxima), a 16-bit key prefix
+//    of it above (two radix passes by one wave, one barrier).  The KC maxima
+//    above tau are KC distinct content scores, so the top KC are all >= tau.
+// 3. Candidates (content scores >= tau), compacted per wave by ballot, so their
+//    order is the same on every run.  Barrier.  Every wave ranks all
+//    candidates exactly (score desc, block asc; adakv/selector.py:18-60) in
+//    registers: candidate lane c holds its rank, and the block of rank r is a
+//    ballot away.  More candidates than two per lane (ties), or KC > 64, take
+//    the general selection instead: an exact radix select over all content
+//    scores.
 // 4. Flash-decode over the head's k blocks on the matrix cores (attend.hpp):
-//    16-token tiles spread over the decode waves, tile i on wave i % DW; the
-//    waves' (m, l, acc) are merged through LDS.  The block count per head is
-//    small (k_max), so one workgroup per head needs no split-K.
+//    16-token item j on wave j % NW, the forced items from the registers they
+//    were loaded into in phase 0.  The waves' (m, l, acc) merge through LDS.
+//
+// Registers stay at or below 256 per wave: a build of this kernel at 329
+// (with the general selection unrolled over a thread's scores) started 2.7 us
+// later after the score kernel than one at 247 (measured with wall-clock
+// stamps), so the general selection is written as plain loops.
 #include <float.h>
 
 #include <algorithm>
@@ -33,32 +46,34 @@
 namespace adakv {
 namespace {
 
-constexpr int kFusedThreads = 512;
-constexpr int kLanesPerHead = 16;            // lanes merging one head's records
-constexpr int kRecsPerLane = 4;              // records a lane loads up front
+constexpr int kFastKC = 16;         // KC up to this: tau by repeated wave maxima
+constexpr int kRadixKC = 64;        // KC up to this: tau by two radix passes (else the general selection)
+constexpr int kCandLanes = 2;       // candidates per lane on the fast path
+constexpr int kRecsUpFront = 4;     // records per lane loaded in phase 0
 
-// Decode waves: all 8.
-template <int D>
-constexpr int fused_decode_waves() { return kFusedThreads / kWave; }
-
-template <int D, int IPT>
-union FusedBig {
-  struct {
-    SelectLds<kFusedThreads> sel;                                  // the selection
-    alignas(16) float sc[kFusedThreads * IPT];                     // and this head's scores
-  } x;
-  uint32_t vt[fused_decode_waves<D>() * TileShape<D>::VT_WORDS];   // then the V tiles
+template <int NT, int D>
+struct StepLds {
+  float maxv[NT];                                             // thread content maxima
+  uint64_t cand[NT / kWave][kCandLanes * kWave];              // candidate keys, per wave
+  int wn[NT / kWave];                                         // candidates per wave (-1: too many)
+  int hist[512];                                              // radix histograms
+  int rd[4];                                                  // radix digit and count above
+  int sc[NT / kWave];                                         // scan scratch
+  float tau;
+  alignas(16) uint64_t keys[kSortCap];                        // general selection: selected keys
+  int list[kSortCap];                                         // content blocks by rank (general path)
+  uint32_t vt[(NT / kWave) * TileShape<D>::VT_WORDS];         // the waves' V tiles
+  float m[NT / kWave], l[NT / kWave];
+  float acc[NT / kWave][D];
 };
 
-template <int D, int IPT>
-constexpr size_t fused_static_lds() {
-  return sizeof(FusedBig<D, IPT>) + kSortCap * sizeof(int) + (2 + D) * fused_decode_waves<D>() * sizeof(float);
-}
-
-// Scores per thread for a max_blocks (0: not served).
-inline int fused_ipt(int max_blocks) {
-  return max_blocks <= kFusedThreads * 4 ? 4 : max_blocks <= kFusedThreads * 8 ? 8
-       : max_blocks <= kFusedThreads * 16 ? 16 : 0;
+// Lanes merging one head's records: the largest power of two with
+// Hq * LPH <= NT, at most 16 (4 for Hq = 64, 8 for Hq = 32 with 256 threads).
+template <int NT>
+__device__ __forceinline__ int lanes_per_head(int Hq) {
+  int l = 16;
+  while (l > 1 && l * Hq > NT) l >>= 1;
+  return l;
 }
 
 // x / d, with s = log2(d) when d is a power of two (else -1).
@@ -69,6 +84,12 @@ __device__ __forceinline__ double readlane_d(double x, int l) {
   const int lo = __builtin_amdgcn_readlane((int)(u & 0xffffffffll), l);
   const int hi = __builtin_amdgcn_readlane((int)(u >> 32), l);
   return __longlong_as_double(((long long)hi << 32) | (uint32_t)lo);
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t x, int l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
 }
 
 // NumPy's pairwise sum of a[0, n) for n <= 128 (the single-block case of
@@ -96,18 +117,181 @@ __device__ __forceinline__ double wave_pairwise_sum(const double* a, int n) {
   return res;
 }
 
-template <int KVDT, int D, int IPT>
-__global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs fa) {
-  constexpr int NT = kFusedThreads, NW = NT / kWave;
-  constexpr int DW = fused_decode_waves<D>();
+// The KC-th largest of mv[0, n) (LDS, n <= NT), by one wave and without any
+// barrier: KC rounds of a wave maximum, each removing one occurrence (equal
+// values count separately).  -FLT_MAX when fewer than KC values are finite
+// maxima (> -inf); every lane receives it.
+template <int NT>
+__device__ __forceinline__ float kth_largest(const float* mv, int n, int KC) {
+  constexpr int PER = NT / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  float x[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) x[i] = lane + kWave * i < n ? mv[lane + kWave * i] : -INFINITY;
+  float kth = -INFINITY;
+  int found = 0;
+  for (int r = 0; r < KC; ++r) {
+    float lm = x[0];
+#pragma unroll
+    for (int i = 1; i < PER; ++i) lm = fmaxf(lm, x[i]);
+    const float wm = wave_allreduce(lm, OpMax());
+    if (wm == -INFINITY) break;
+    const uint64_t holders = __ballot(lm == wm);
+    if (lane == (int)__builtin_ctzll(holders)) {
+      bool done = false;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const bool hit = !done && x[i] == wm;
+        x[i] = hit ? -INFINITY : x[i];
+        done = done || hit;
+      }
+    }
+    kth = wm;
+    ++found;
+  }
+  return found == KC ? fmaxf(kth, -FLT_MAX) : -FLT_MAX;
+}
+
+// A lower bound of the KC-th largest of mv[0, n), by one wave (its own LDS
+// histograms, no workgroup barrier): two radix passes over the order-
+// preserving keys of the values (the top byte, then the next byte within the
+// bin that holds the KC-th largest) give the 16-bit key prefix of the KC-th
+// largest; the bound is the smallest float with that prefix.  -FLT_MAX when
+// fewer than KC values are finite (> -inf).
+__device__ __forceinline__ float kth_largest_radix(const float* mv, int n, int KC, int* hist, int* rd) {
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int i = lane; i < 512; i += kWave) hist[i] = 0;
+  __builtin_amdgcn_wave_barrier();             // a wave's LDS operations complete in order
+  for (int i = lane; i < n; i += kWave) {
+    const float x = mv[i];
+    if (x != -INFINITY) atomicAdd(&hist[(uint32_t)(sel_key(x, 0) >> 32) >> 24], 1);
+  }
+  __builtin_amdgcn_wave_barrier();
+  radix_digit(hist, KC, rd);                   // rd[0] = digit, rd[1] = count above
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t b1 = (uint32_t)rd[0];
+  const int above1 = rd[1];
+  for (int i = lane; i < n; i += kWave) {
+    const float x = mv[i];
+    const uint32_t key = (uint32_t)(sel_key(x, 0) >> 32);
+    if (x != -INFINITY && (key >> 24) == b1) atomicAdd(&hist[256 + ((key >> 16) & 0xffu)], 1);
+  }
+  __builtin_amdgcn_wave_barrier();
+  radix_digit(hist + 256, KC - above1, rd + 2);
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t tk = (b1 << 24) | ((uint32_t)rd[2] << 16);
+  const uint32_t u = (tk & 0x80000000u) ? (tk & 0x7fffffffu) : ~tk;
+  return (above1 < 0 || rd[3] < 0) ? -FLT_MAX : fmaxf(__uint_as_float(u), -FLT_MAX);
+}
+
+// The general selection (rare: ties leave more candidates than the fast path
+// holds, or KC > 64), by all NT threads: the exact top KC content blocks by an
+// MSB-first radix select over the 32-bit keys of the sanitised scores,
+// re-read from memory (four 8-bit passes), the blocks at the boundary key
+// taken lowest block first; the KC selected (score, block) keys are sorted
+// descending and emit(r, block) is called for every rank r < KC.  Plain loops
+// keep the path small.  KC <= kSortCap and KC <= the number of content blocks.
+template <int NT, int IPT, int D, typename Emit>
+__device__ void select_general(StepLds<NT, D>& L, const float* srow, int sp, int c_lo, int c_hi, int base, int KC,
+                               Emit&& emit) {
+  const int tid = threadIdx.x;
+  auto score = [&](int i) { return sanitize(srow[min(base + i, sp - 1)]); };
+  auto is_c = [&](int i) { return base + i >= c_lo && base + i < c_hi; };
+  auto key32 = [&](int i) { return (uint32_t)(sel_key(score(i), 0) >> 32); };
+  uint32_t prefix = 0;
+  int need = KC;
+#pragma unroll 1
+  for (int pass = 0; pass < 4; ++pass) {
+    const int sh = 24 - 8 * pass;
+    for (int j = tid; j < 256; j += NT) L.hist[j] = 0;
+    lds_barrier();
+#pragma unroll 1
+    for (int i = 0; i < IPT; ++i) {
+      if (!is_c(i)) continue;
+      const uint32_t k = key32(i);
+      if (pass == 0 || (k >> (sh + 8)) == prefix) atomicAdd(&L.hist[(k >> sh) & 255u], 1);
+    }
+    lds_barrier();
+    if (tid < kWave) radix_digit(L.hist, need, L.rd);
+    lds_barrier();
+    prefix = (prefix << 8) | (uint32_t)L.rd[0];
+    need -= L.rd[1];
+  }
+  // prefix is the boundary key: every block above it and the lowest-index
+  // `need` of the blocks equal to it
+  int n_eq = 0;
+#pragma unroll 1
+  for (int i = 0; i < IPT; ++i) n_eq += (is_c(i) && key32(i) == prefix) ? 1 : 0;
+  int tot;
+  const int eq_before = block_excl_scan<NT>(n_eq, L.sc, &tot);
+  int n_sel = 0;
+  {
+    int e = eq_before;
+#pragma unroll 1
+    for (int i = 0; i < IPT; ++i) {
+      if (!is_c(i)) continue;
+      const uint32_t k = key32(i);
+      if (k > prefix) ++n_sel;
+      else if (k == prefix) n_sel += (e++ < need) ? 1 : 0;
+    }
+  }
+  int o = block_excl_scan<NT>(n_sel, L.sc, &tot);   // tot == KC
+  {
+    int e = eq_before;
+#pragma unroll 1
+    for (int i = 0; i < IPT; ++i) {
+      if (!is_c(i)) continue;
+      const uint32_t k = key32(i);
+      const bool take = k > prefix || (k == prefix && e++ < need);
+      if (take && o < kSortCap) L.keys[o++] = sel_key(score(i), base + i);
+    }
+  }
+  const int n = next_pow2(max(tot, 1));
+  for (int i = tot + tid; i < n; i += NT) L.keys[i] = 0;
+  __syncthreads();
+  bitonic_desc<NT>(L.keys, n);
+  for (int r = tid; r < KC; r += NT) emit(r, key_index(L.keys[r]));
+}
+
+// The KC-th largest of one value per lane (x), by repeated wave maxima that
+// remove one occurrence each; -FLT_MAX when fewer than KC values are finite
+// (> -inf).  Every lane receives it.
+__device__ __forceinline__ float kth_of_lanes(float x, int KC) {
+  const int lane = threadIdx.x & (kWave - 1);
+  float kth = -INFINITY;
+  int found = 0;
+  for (int r = 0; r < KC; ++r) {
+    const float wm = wave_allreduce(x, OpMax());
+    if (wm == -INFINITY) break;
+    const uint64_t holders = __ballot(x == wm);
+    if (lane == (int)__builtin_ctzll(holders)) x = -INFINITY;
+    kth = wm;
+    ++found;
+  }
+  return found == KC ? fmaxf(kth, -FLT_MAX) : -FLT_MAX;
+}
+
+__device__ __forceinline__ int wave_min_int(int x) {
+  auto mn = [](int a, int b) { return a < b ? a : b; };
+  x = mn(x, __float_as_int(dpp_mov<0xB1>(__int_as_float(x))));
+  x = mn(x, __float_as_int(dpp_mov<0x4E>(__int_as_float(x))));
+  x = mn(x, __float_as_int(dpp_mov<0x141>(__int_as_float(x))));
+  x = mn(x, __float_as_int(dpp_mov<0x140>(__int_as_float(x))));
+  LanePair p = swap16(__int_as_float(x));
+  x = mn(__float_as_int(p.a), __float_as_int(p.b));
+  p = swap32(__int_as_float(x));
+  return mn(__float_as_int(p.a), __float_as_int(p.b));
+}
+
+template <int KVDT, int D, int NT, int IPT>
+__global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
+  warm_kernargs<sizeof(FusedArgs) + 8>();
+  constexpr int NW = NT / kWave;
   constexpr int NT16 = TileShape<D>::NT16;
-  constexpr int LPH = kLanesPerHead, HPW = kWave / LPH, RPL = kRecsPerLane;
   using Mask = MaskT<IPT>;
   constexpr Mask kOne = 1;
-  __shared__ __align__(16) FusedBig<D, IPT> big;
-  __shared__ int s_list[kSortCap];          // content blocks by rank
-  __shared__ float s_m[DW], s_l[DW];
-  __shared__ float s_acc[DW][D];            // the decode waves' accumulators for the merge
+  constexpr int kPool = 9;                   // candidate entries per lane: 4 sub-chunks x 2, one appended row
+  __shared__ __align__(16) StepLds<NT, D> L;
   extern __shared__ double s_w[];            // [Hq] budget weights of the sequence's heads
 
   const SelectArgs& a = fa.s;
@@ -115,20 +299,23 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
   // XCD-aware placement: workgroups are dealt to the 8 XCDs in turn (linear id
   // mod 8), so linear id i takes position (i mod 8) * n/8 + i / 8 of the
   // (sequence, q-head) order: each XCD holds consecutive q-heads -- the heads
-  // of a KV group, the sequences' records and their shared sink, local and
-  // common blocks then meet in one L2.
+  // of a KV group, whose sink, local and shared blocks then meet in one L2.
   int h, b;
   {
     const int n = gridDim.x * gridDim.y, i = blockIdx.y * gridDim.x + blockIdx.x;
     const int pos = (n & 7) == 0 ? (i & 7) * (n >> 3) + (i >> 3) : i;
-    h = pos % gridDim.x;
-    b = pos / gridDim.x;
+    // (uniform values kept in scalar registers: a length loaded from memory
+    // or a division expanded on the vector unit would otherwise drag every
+    // bound and address derived from it onto the vector unit)
+    h = __builtin_amdgcn_readfirstlane(pos % gridDim.x);
+    b = __builtin_amdgcn_readfirstlane(pos / gridDim.x);
   }
   const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1), w = tid / kWave;
+  const int lane = tid & (kWave - 1);
+  const int wu = __builtin_amdgcn_readfirstlane(tid / kWave);   // the wave index, provably uniform
   const int col = lane & 15, grp = lane >> 4;
   const int Hq = a.Hq;
-  const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
+  const int len = __builtin_amdgcn_readfirstlane(seq_len_of(a.seq_lens, a.uniform_len, b));
   const int nb = len > 0 ? div_p2(len + a.bs - 1, a.bs, a.bs_shift) : 0;
   const Bounds bb = budget_bounds(nb, a.cfg);
   const int nf = bb.n_forced;
@@ -144,59 +331,41 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
     for (int i = tid; i < D; i += NT) store_elt(d.out, d.odt, oo + i, __builtin_nanf(""));
     return;
   }
-  select_init(big.x.sel);
 
-  // ---- 1. loads ----
-  // Every load here is unconditional, its index clamped in bounds (values not
-  // wanted are discarded where they are consumed): a load under a branch makes
-  // the compiler wait for it where the branches join.
-  //
-  // (a) the records of each 16-lane row's head (RPL per lane, the rest later
-  //     if a head has more): all heads when the budget is adaptive (four per
-  //     wave and pass), else only this head (for its content maxima), and the
-  //     score of one row no record covers (the decode-time append).
+  // ---- 0. loads, each with its index clamped in bounds ----
+  // (a) the softmax partials of this lane's head: head tid / LPH, records hl, hl + LPH, ...
   const int first_app = a.n_new > 0 ? div_p2(max(len - a.n_new, 0), a.bs, a.bs_shift) : nb;
   const int rows_in_chunks = min(nb, first_app);
-  const int n_ck = (rows_in_chunks + a.chunk_rows - 1) >> a.chunk_shift;   // records
+  const int n_ck = (rows_in_chunks + a.chunk_rows - 1) >> a.chunk_shift;   // records per head
   const int n_extra = nb - rows_in_chunks;                                 // rows no record covers
-  const float tf = (float)fmax(a.cfg.temperature, 1e-6);
-  const int hl = lane % LPH;
-  auto head_of = [&](int p) -> int {
-    if (adaptive) return (p * NW + w) * HPW + lane / LPH;
-    return (w == 0 && lane < LPH) ? h : -1;
-  };
-  // per-lane offsets stay 32-bit (the host bounds Hq * pitch)
+  const int LPH = lanes_per_head<NT>(Hq);
+  const int hl = tid & (LPH - 1);
   const float* parts_b = a.parts + (int64_t)b * Hq * a.parts_pitch * kPartFloats;
   const float* scores_b = a.scores + (int64_t)b * Hq * a.sp;
-  auto rec = [&](int hh, int j) {
-    return reinterpret_cast<const float4*>(parts_b + (hh * a.parts_pitch + min(j, max(n_ck - 1, 0))) * kPartFloats);
+  auto rec4 = [&](int hh, int j, int g) {    // 16-byte group g of record j of head hh
+    return *reinterpret_cast<const float4*>(parts_b + (hh * a.parts_pitch + min(j, max(n_ck - 1, 0))) * kPartFloats +
+                                            4 * g);
   };
-  auto extra = [&](int hh, int e) { return scores_b + hh * a.sp + min(rows_in_chunks + e, nb - 1); };
-  const int hh0 = head_of(0);
-  const int hs0 = (hh0 >= 0 && hh0 < Hq) ? hh0 : h;
-  float4 R0[RPL], R1[RPL];
+  auto extra = [&](int hh, int e) { return scores_b[hh * a.sp + min(rows_in_chunks + e, nb - 1)]; };
+  const int hh0 = tid / LPH;
+  const int hs0 = min(hh0, Hq - 1);
+  float4 R[kRecsUpFront];
 #pragma unroll
-  for (int u = 0; u < RPL; ++u) {
-    R0[u] = rec(hs0, hl + LPH * u)[0];
-    R1[u] = rec(hs0, hl + LPH * u)[1];
-  }
-  const float X0 = *extra(hs0, hl);
+  for (int u = 0; u < kRecsUpFront; ++u) R[u] = rec4(hs0, hl + LPH * u, 0);
+  const float X0 = extra(hs0, hl);
+  // the nucleus policy's weights, written by the nucleus kernel before this launch
+  const double W0 = a.wbuf[(int64_t)b * Hq + min(tid, Hq - 1)];
   __builtin_amdgcn_sched_barrier(0);
-  // (b) this head's scores: thread t owns blocks [t*IPT, (t+1)*IPT); rows
-  //     past nb (stale) are never content
-  float v[IPT];
-  {
-    const float* srow = scores_b + h * a.sp;
-#pragma unroll
-    for (int i = 0; i < IPT; i += 4) {
-      const float4 f = *reinterpret_cast<const float4*>(srow + min(tid * IPT + i, a.sp - 4));
-      v[i] = f.x; v[i + 1] = f.y; v[i + 2] = f.z; v[i + 3] = f.w;
-    }
-  }
+  // (b) this head's candidate pool (every wave holds all of it): lane l the
+  //     top two of the 4 sub-chunks of record l, their bounds, and appended
+  //     row l (the pool serves heads with at most 64 records)
+  const bool pool_ok = n_ck <= kWave && n_extra <= kWave;
+  const float4 C1 = rec4(h, lane, 1), C2 = rec4(h, lane, 2), C3 = rec4(h, lane, 3), C4 = rec4(h, lane, 4);
+  const float XE = extra(h, lane);
   __builtin_amdgcn_sched_barrier(0);
   // (c) the query (same 16-bit type as K, 16-byte aligned rows), as the B
-  //     operand of S^T: lane (col, grp) holds q[D/4*grp + 8*s .. +7] in
-  //     every column (columns other than 0 are masked out of the softmax)
+  //     operand of S^T: lane (col, grp) holds q[D/4*grp + 8*s .. +7] in every
+  //     column (columns other than 0 are masked out of the softmax)
   uint4 qf[D / 32];
   {
     const uint16_t* qp = reinterpret_cast<const uint16_t*>(d.q) + (int64_t)b * d.qsb + (int64_t)h * d.qsh + (D / 4) * grp;
@@ -204,282 +373,478 @@ __global__ __launch_bounds__(kFusedThreads) void select_decode_kernel(FusedArgs 
     for (int s2 = 0; s2 < D / 32; ++s2) qf[s2] = *reinterpret_cast<const uint4*>(qp + 8 * s2);
   }
   __builtin_amdgcn_sched_barrier(0);
-  // (d) the decode's addressing: item i (16-token sub-tile i % n_sub of list
-  //     entry i / n_sub) belongs to decode wave i % DW; the first n_forced
-  //     entries are the sink blocks then the local blocks, as in the table row
+  // (d) the decode's items: item j is 16-token sub-tile j % n_sub of list
+  //     entry j / n_sub; entries [0, nf) are the sink then the local blocks
+  //     (the table row's order), later ones the content blocks by rank.  The
+  //     first two items of this wave, when forced, are loaded now (only the
+  //     waves that own such an item load it: a CU takes in 64 bytes per
+  //     clock, so a load for nothing delays the useful loads of its other waves)
   const int n_sub = (a.bs + 15) >> 4;
   const int nf_items = nf * n_sub;
   const int64_t head_off = ((int64_t)b * d.sb + (int64_t)(h / d.G) * d.sh + (D / 4) * grp) * 2;
   const char* kbase = reinterpret_cast<const char*>(d.k) + head_off;
   const char* vbase = reinterpret_cast<const char*>(d.v) + head_off;
   const int64_t row_bytes = d.ss * 2;
-  auto item = [&](int j, int& t0, int& t_hi) {
-    const int e = n_sub == 1 ? j : j / n_sub, sub = j - e * n_sub;
-    const int blk = e < bb.sink ? e : (e < nf ? local_lo + (e - bb.sink) : s_list[e - nf]);
+  auto tokens = [&](int blk, int sub, int& t0, int& t_hi) {
     t0 = blk * a.bs + sub * 16;
     t_hi = min(min(blk * a.bs + a.bs, len), t0 + 16);
   };
-  // the forced tiles of the prefetch path (below): known before any selection
-  const int wu = __builtin_amdgcn_readfirstlane(w);   // the wave index, provably uniform
-  const bool pf_shape = n_sub == 1 && nf <= DW;
-  const bool p_load = pf_shape && wu < nf;
-  TileBuf<D> P;
-  int p0 = 0, p1 = 1;
-  if (p_load) {
-    item(wu, p0, p1);
-    tile_load<D>(kbase, vbase, row_bytes, p0, p1, P);
+  auto forced_block = [&](int e) { return e < bb.sink ? e : local_lo + (e - bb.sink); };
+  // PF forced items per wave are prefetched (none with 512 threads: 8 waves
+  // already cover the forced items, and two waves per SIMD halve the register file)
+  constexpr int PF = NT == 256 ? 2 : 0;
+  TileBuf<D> P0, P1;
+  int p00 = 0, p01 = 1, p10 = 0, p11 = 1;
+  if constexpr (PF >= 1) {
+    if (wu < nf_items) {
+      tokens(forced_block(wu / n_sub), wu % n_sub, p00, p01);
+      tile_load<D>(kbase, vbase, row_bytes, p00, p01, P0);
+    }
+  }
+  if constexpr (PF >= 2) {
+    if (wu + NW < nf_items) {
+      tokens(forced_block((wu + NW) / n_sub), (wu + NW) % n_sub, p10, p11);
+      tile_load<D>(kbase, vbase, row_bytes, p10, p11, P1);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   const double lognb = log((double)max(nb, 2));   // while the loads are in flight
 
-  // ---- 2. entropy weights and this head's content maxima ----
-  // Maxima of record j at 4j .. 4j+3, of row e no record covers at 4*n_ck + e.
-  // one head per 16-lane row: merge its records (and rows no record covers)
-  auto merge_head = [&](int hh, const float4 (&Q0)[RPL], const float4 (&Q1)[RPL], float X) {
-    const bool on = hh >= 0 && hh < Hq;
+  // ---- 1. weights of every head; the pool's first ranks ----
+  const float tf = (float)fmax(a.cfg.temperature, 1e-6);
+  auto merge_head = [&](int hh, const float4 (&Q)[kRecsUpFront], float X) {
+    const bool on = hh < Hq;
     SoftPart pt = soft_empty();
     if (on) {
-      const bool own = hh == h;
-      auto take_rec = [&](int j, const float4& q0, const float4& q1) {
-        pt = soft_merge(pt, SoftPart{q0.x, q0.y, q0.z});
-        if (own) {
-          const float mx[4] = {q0.w, q1.x, q1.y, q1.z};
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (4 * j + i < NT) big.x.sel.maxv[4 * j + i] = mx[i];
-        }
-      };
-      auto take_row = [&](int e, float x) {
+      for (int u = 0; u < kRecsUpFront; ++u)
+        if (hl + LPH * u < n_ck) pt = soft_merge(pt, SoftPart{Q[u].x, Q[u].y, Q[u].z});
+      for (int j = hl + LPH * kRecsUpFront; j < n_ck; j += LPH) {   // long contexts
+        const float4 q4 = rec4(hh, j, 0);
+        pt = soft_merge(pt, SoftPart{q4.x, q4.y, q4.z});
+      }
+      if (hl < n_extra) pt = soft_merge(pt, SoftPart{tf == 1.f ? X : __fdiv_rn(X, tf), 1.f, 0.f});
+      for (int e = hl + LPH; e < n_extra; e += LPH) {
+        const float x = extra(hh, e);
         pt = soft_merge(pt, SoftPart{tf == 1.f ? x : __fdiv_rn(x, tf), 1.f, 0.f});
-        const int r = rows_in_chunks + e, t = 4 * n_ck + e;
-        if (own && t < NT) big.x.sel.maxv[t] = (r >= c_lo && r < c_hi) ? sanitize(x) : -INFINITY;
-      };
-#pragma unroll
-      for (int u = 0; u < RPL; ++u)
-        if (hl + LPH * u < n_ck) take_rec(hl + LPH * u, Q0[u], Q1[u]);
-      for (int j = hl + LPH * RPL; j < n_ck; j += LPH) take_rec(j, rec(hh, j)[0], rec(hh, j)[1]);   // long heads
-      if (hl < n_extra) take_row(hl, X);
-      for (int e = hl + LPH; e < n_extra; e += LPH) take_row(e, *extra(hh, e));
+      }
     }
-    pt = soft_group_merge<LPH>(pt);
-    if (adaptive && on && hl == 0) s_w[hh] = entropy_weight(pt, lognb);
+    switch (LPH) {                          // uniform
+      case 16: pt = soft_group_merge<16>(pt); break;
+      case 8: pt = soft_group_merge<8>(pt); break;
+      case 4: pt = soft_group_merge<4>(pt); break;
+      case 2: pt = soft_group_merge<2>(pt); break;
+      default: break;
+    }
+    if (on && hl == 0) s_w[hh] = entropy_weight(pt, lognb);
   };
-  // the first pass consumes the records loaded up front, in place
-  merge_head(hh0, R0, R1, X0);
-  if (nucleus)                               // written by the nucleus kernel before this launch
-    for (int hh = tid; hh < Hq; hh += NT) s_w[hh] = a.wbuf[(int64_t)b * Hq + hh];
-  const int passes = adaptive ? ceil_div(Hq, HPW * NW) : 1;
-  for (int p = 1; p < passes; ++p) {         // more than 32 heads
-    const int hh = head_of(p);
-    const int hs = (hh >= 0 && hh < Hq) ? hh : h;
-    float4 Q0[RPL], Q1[RPL];
+  if (adaptive) {
+    merge_head(hh0, R, X0);
+    for (int p = 1; p * (NT / LPH) < Hq; ++p) {    // more heads than NT / LPH
+      const int hh = p * (NT / LPH) + tid / LPH;
+      const int hs = min(hh, Hq - 1);
+      float4 Q[kRecsUpFront];
 #pragma unroll
-    for (int u = 0; u < RPL; ++u) { Q0[u] = rec(hs, hl + LPH * u)[0]; Q1[u] = rec(hs, hl + LPH * u)[1]; }
-    merge_head(hh, Q0, Q1, *extra(hs, hl));
+      for (int u = 0; u < kRecsUpFront; ++u) Q[u] = rec4(hs, hl + LPH * u, 0);
+      merge_head(hh, Q, extra(hs, hl));
+    }
+  } else if (nucleus) {
+    if (tid < Hq) s_w[tid] = W0;
+    for (int hh = tid + NT; hh < Hq; hh += NT) s_w[hh] = a.wbuf[(int64_t)b * Hq + hh];
   }
-  // this head's scores to LDS (the selection reads them there, so they hold
-  // no registers while the tiles are prefetched), this thread's content bits
-  // and its largest sanitised content score
-  const int base = tid * IPT;
-  Mask content = 0;
-  float vmax = -INFINITY;
+  // The pool: entries (score, block) of this lane; every content block outside
+  // it scores at most the largest bound of its sub-chunk.
+  float pv[kPool];
+  int pr[kPool];
+  float bound;
+  {
+    const bool rl = lane < n_ck;
+    const float v1[4] = {C1.x, C1.y, C1.z, C1.w}, v2[4] = {C2.x, C2.y, C2.z, C2.w};
+    const float v3[4] = {C3.x, C3.y, C3.z, C3.w};
+    const uint32_t rr[4] = {__float_as_uint(C4.x), __float_as_uint(C4.y), __float_as_uint(C4.z), __float_as_uint(C4.w)};
+    bound = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < IPT; ++i) {
-    const bool is_c = base + i >= c_lo && base + i < c_hi;
-    if (is_c) content |= kOne << i;
-    vmax = fmaxf(vmax, is_c ? sanitize(v[i]) : -INFINITY);
+    for (int sc = 0; sc < 4; ++sc) {
+      pv[2 * sc] = rl ? v1[sc] : -INFINITY;
+      pv[2 * sc + 1] = rl ? v2[sc] : -INFINITY;
+      pr[2 * sc] = (int)(rr[sc] & 0xffffu);
+      pr[2 * sc + 1] = (int)(rr[sc] >> 16);
+      bound = fmaxf(bound, rl ? v3[sc] : -INFINITY);
+    }
+    const int re = rows_in_chunks + lane;
+    pv[8] = (lane < n_extra && re >= c_lo && re < c_hi) ? sanitize(XE) : -INFINITY;
+    pr[8] = re;
   }
+  bound = wave_allreduce(bound, OpMax());
+  // lane maximum (score, then lowest block among equal scores)
+  float lm = pv[0];
 #pragma unroll
-  for (int i = 0; i < IPT; i += 4)
-    *reinterpret_cast<float4*>(&big.x.sc[base + i]) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+  for (int e = 1; e < kPool; ++e) lm = fmaxf(lm, pv[e]);
+  int lr = 0x7fffffff;
+#pragma unroll
+  for (int e = 0; e < kPool; ++e) lr = (pv[e] == lm && pr[e] < lr) ? pr[e] : lr;
+  // Ranks of the pool's top K: the candidates are the entries >= the K-th
+  // largest lane maximum (at least K of them, the top K among them),
+  // compacted in lane order into this wave's LDS list, then lane c holds
+  // candidate c's key and rank.  Returns the number of candidates (-1: more
+  // than a wave holds).
+  uint64_t pk = 0;
+  int prank = 1 << 30;
+  auto pool_rank = [&](int K) -> int {
+    const float tau = kth_of_lanes(lm, K);
+    int c = 0;
+#pragma unroll
+    for (int e = 0; e < kPool; ++e) c += (pv[e] >= tau && pv[e] != -INFINITY) ? 1 : 0;
+    const int incl = wave_incl_scan(c);
+    const int n_c = __builtin_amdgcn_readlane(incl, kWave - 1);
+    if (n_c > kWave) return -1;
+    if (c == 1) {
+      L.cand[wu][incl - 1] = sel_key(lm, lr);        // the lane maximum is its one candidate
+    } else if (c > 1) {
+      int o = incl - c;
+#pragma unroll
+      for (int e = 0; e < kPool; ++e)
+        if (pv[e] >= tau && pv[e] != -INFINITY) L.cand[wu][o++] = sel_key(pv[e], pr[e]);
+    }
+    __builtin_amdgcn_wave_barrier();                  // this wave's LDS writes are read back in order
+    pk = lane < n_c ? L.cand[wu][lane] : 0ull;
+    int r = 0;
+    for (int j = 0; j < n_c; ++j) r += readlane_u64(pk, j) > pk;
+    prank = lane < n_c ? r : 1 << 30;
+    __builtin_amdgcn_wave_barrier();                  // reads done before the list is rewritten
+    return n_c;
+  };
+  // the first NW ranks now, and this wave's content tile of the decode: rank
+  // rho (content item rho is item nf_items + rho, on wave (nf_items + rho) % NW)
+  const int rho = (wu - nf_items % NW + NW) % NW;
+  int n_pre = -1;
+  TileBuf<D> CA;
+  int ca0 = 0, ca1 = 1, cablk = -1;
+  if (pool_ok) {
+    n_pre = pool_rank(NW);
+    if (n_sub == 1 && rho < n_pre) {
+      const uint64_t hit = __ballot(prank == rho);
+      cablk = min(max(key_index(readlane_u64(pk, (int)__builtin_ctzll(hit))), 0), nb - 1);
+      tokens(cablk, 0, ca0, ca1);
+      tile_load<D>(kbase, vbase, row_bytes, ca0, ca1, CA);
+    }
+  }
   lds_barrier();
 
-  // ---- 3. the head's count and selection ----
-  // every wave evaluates the sum of weights in NumPy's order
+  // ---- 2. the head's count (every wave) ----
   const bool weighted = adaptive || nucleus;
   const double wsum = !weighted ? 0.0 : Hq <= 128 ? wave_pairwise_sum(s_w, Hq) : numpy_pairwise_sum<6>(s_w, Hq);
   const int k = min(head_count(bb, a.cfg.policy, weighted ? s_w[h] : 0.0, wsum, Hq), a.T);
+  const int KC = max(k - nf, 0);
   if (tid == 0) {
     if (d.sel_lens_out) d.sel_lens_out[(int64_t)b * Hq + h] = k;
     if (adaptive) a.wbuf[(int64_t)b * Hq + h] = s_w[h];
   }
-  const int KC = max(k - nf, 0);
-  for (int j = tid; j < nf; j += NT) trow[j] = j < bb.sink ? j : local_lo + (j - bb.sink);
+  for (int j = tid; j < nf; j += NT) trow[j] = forced_block(j);
   for (int j = k + tid; j < a.T; j += NT) trow[j] = -1;
-  // Prefetch: with one tile per block, the forced blocks on their own waves
-  // and at most DW candidates, wave w holds forced block w (w < nf, loaded in
-  // the prologue) and loads candidate (w - nf) mod DW as soon as the
-  // candidates are known, before they are ranked; after the rank it computes
-  // the candidate if its rank is < KC (the decode does not depend on the
-  // order of the blocks).  Only the waves that own a tile issue loads.
-  bool prefetched = false;
-  TileBuf<D> C;
-  int c0 = 0, c1 = 1, cand = -1;
-  if (KC > 0) {
-    if (w == 0) select_threshold(big.x.sel, KC, min(4 * n_ck + n_extra, NT));
-    lds_barrier();
-    select_content<NT, IPT>(
-        big.x.sel, [&](int i) { return big.x.sc[base + i]; }, content, base, KC, vmax,
-        [&](int r, int blk) {
-          s_list[r] = blk;
-          trow[nf + r] = blk;
-        },
-        [&](int n_cand) {
-          prefetched = pf_shape && n_cand <= DW;
-          const int c = (wu - nf % DW + DW) % DW;
-          if (prefetched && wu < DW && c < n_cand) {
-            const int blk = key_index(big.x.sel.keys[c]);
-            c0 = blk * a.bs;
-            c1 = min(c0 + a.bs, len);
-            tile_load<D>(kbase, vbase, row_bytes, c0, c1, C);
-            cand = c;
-          }
-        });
+
+  // ---- 3. the content selection ----
+  // pool path: the top KC of the pool, exact when no content block outside
+  // it can rank among them: every bound below the KC-th score
+  bool use_pool = false;
+  if (KC > 0 && pool_ok && KC <= kFastKC) {
+    const int n_c = KC <= NW ? n_pre : pool_rank(KC);
+    if (n_c >= KC) {
+      const uint64_t hit = __ballot(prank == KC - 1);
+      const uint64_t kth = readlane_u64(pk, (int)__builtin_ctzll(hit));
+      const uint32_t u = (uint32_t)(kth >> 32);     // the KC-th score, back from its order-preserving bits
+      const float v_kth = __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+      use_pool = bound < v_kth;
+    }
+    if (use_pool && wu == 0 && prank < KC) trow[nf + prank] = key_index(pk);
   }
-  const bool c_take = cand >= 0 && big.x.sel.rank[cand] < KC;   // read before the LDS is reused
-  lds_barrier();                           // s_list complete; the selection's LDS becomes the V tiles
+  // full path: every score of the head (thread t owns blocks [t*IPT,
+  // (t+1)*IPT)); its own candidates (ck, cr) or the general selection's list
+  constexpr int kBig = 1 << 30;
+  bool fast = false;
+  uint64_t ck0 = 0, ck1 = 0;
+  int cr0 = kBig, cr1 = kBig;
+  int n_own = 0, own0 = 0;
+  if (KC > 0 && !use_pool) {
+    const int base = tid * IPT;
+    float v[IPT];
+    {
+      const float* srow = scores_b + h * a.sp;
+#pragma unroll
+      for (int i = 0; i < IPT; i += 4) {
+        const float4 f = *reinterpret_cast<const float4*>(srow + min(base + i, a.sp - 4));
+        v[i] = f.x; v[i + 1] = f.y; v[i + 2] = f.z; v[i + 3] = f.w;
+      }
+    }
+    Mask content;
+    float vmax;
+    if (base >= c_lo && base + IPT <= c_hi) {
+      // every block of the thread is content: sanitize() of the plain maximum
+      // (fmaxf skips NaN, which sanitize() maps to its lowest value anyway)
+      float mx = v[0];
+#pragma unroll
+      for (int i = 1; i < IPT; ++i) mx = fmaxf(mx, v[i]);
+      vmax = sanitize(mx);
+      content = (Mask)~Mask(0) >> (8 * sizeof(Mask) - IPT);
+    } else {
+      content = 0;
+      vmax = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < IPT; ++i) {
+        const bool is_c = base + i >= c_lo && base + i < c_hi;
+        if (is_c) content |= kOne << i;
+        vmax = fmaxf(vmax, is_c ? sanitize(v[i]) : -INFINITY);
+      }
+    }
+    L.maxv[tid] = vmax;
+    lds_barrier();
+    fast = KC <= kRadixKC;
+    if (fast) {
+      float tau;
+      if (KC <= kFastKC) {
+        tau = kth_largest<NT>(L.maxv, NT, KC);
+      } else {
+        if (wu == 0) {
+          const float t = kth_largest_radix(L.maxv, NT, KC, L.hist, L.rd);
+          if (lane == 0) L.tau = t;
+        }
+        lds_barrier();
+        tau = L.tau;
+      }
+      Mask cm = 0;
+      if (vmax >= tau) {
+        if (tau == -FLT_MAX) {               // the bottom of the range: compare sanitised scores
+#pragma unroll
+          for (int i = 0; i < IPT; ++i) cm |= (sanitize(v[i]) >= tau) ? (kOne << i) : Mask(0);
+        } else {
+#pragma unroll
+          for (int i = 0; i < IPT; ++i) cm |= (v[i] >= tau) ? (kOne << i) : Mask(0);
+        }
+        cm &= content;
+      }
+      // per-wave compaction in lane order (the same order on every run)
+      constexpr int kCap = kCandLanes * kWave;
+      const int c = popcnt(cm);
+      const int incl = wave_incl_scan(c);
+      const int wtot = __builtin_amdgcn_readlane(incl, kWave - 1);
+      if (wtot <= kCap && c == 1) {
+        // one candidate: it is the thread's largest content score (that is >= tau)
+        L.cand[wu][incl - 1] = sel_key(vmax, base + (int)__builtin_ctzll((uint64_t)cm));
+      } else if (wtot <= kCap && c > 1) {   // ties and close scores: rare
+        int o = incl - c;
+#pragma unroll
+        for (int i = 0; i < IPT; ++i)
+          if ((cm >> i) & kOne) L.cand[wu][o++] = sel_key(sanitize(v[i]), base + i);
+      }
+      if (lane == 0) L.wn[wu] = wtot <= kCap ? wtot : -1;
+      lds_barrier();
+      int n_cand = 0;
+      bool over = false;
+      int wn[NW];
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) {
+        wn[ww] = L.wn[ww];
+        over = over || wn[ww] < 0;
+        n_cand += max(wn[ww], 0);
+      }
+      fast = !over && n_cand <= kCap;
+      n_own = max(wn[wu], 0);
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) own0 += ww < wu ? max(wn[ww], 0) : 0;
+      if (fast) {
+        auto fetch = [&](int idx) -> uint64_t {   // candidate idx of the concatenated lists
+          int src = 0;
+#pragma unroll
+          for (int ww = 0; ww < NW - 1; ++ww)
+            if (src == ww && idx >= wn[ww]) { idx -= wn[ww]; src = ww + 1; }
+          return L.cand[src][min(idx, kCap - 1)];
+        };
+        ck0 = lane < n_cand ? fetch(lane) : 0ull;
+        ck1 = lane + kWave < n_cand ? fetch(lane + kWave) : 0ull;
+        int r0 = 0, r1 = 0;
+        const int n0 = min(n_cand, kWave);
+        for (int j = 0; j < n0; ++j) {
+          const uint64_t kj = readlane_u64(ck0, j);
+          r0 += kj > ck0;
+          r1 += kj > ck1;
+        }
+        for (int j = kWave; j < n_cand; ++j) {
+          const uint64_t kj = readlane_u64(ck1, j - kWave);
+          r0 += kj > ck0;
+          r1 += kj > ck1;
+        }
+        cr0 = lane < n_cand ? r0 : kBig;
+        cr1 = lane + kWave < n_cand ? r1 : kBig;
+        if (wu == 0) {
+          if (cr0 < KC) trow[nf + cr0] = key_index(ck0);
+          if (cr1 < KC) trow[nf + cr1] = key_index(ck1);
+        }
+      }
+    }
+    if (!fast) {
+      select_general<NT, IPT, D>(L, scores_b + h * a.sp, a.sp, c_lo, c_hi, base, KC, [&](int r, int blk) {
+        L.list[r] = blk;
+        trow[nf + r] = blk;
+      });
+      lds_barrier();
+    }
+  }
 
   // ---- 4. flash-decode over the k blocks ----
   TileState<D> st;
   tile_init(st);
-  const int n_items = k * n_sub;
-  if (w < DW) {
-    uint32_t* vt = big.vt + w * TileShape<D>::VT_WORDS;
+  {
+    uint32_t* vt = L.vt + wu * TileShape<D>::VT_WORDS;
     const float scale = d.scale_log2;
-    auto load = [&](int t0, int t_hi, TileBuf<D>& r) { tile_load<D>(kbase, vbase, row_bytes, t0, t_hi, r); };
     auto compute = [&](int t0, int t_hi, const TileBuf<D>& r) {
       tile_update<KVDT, D>(st, r, qf, vt, t0, t_hi, col == 0, scale);
     };
-    const int mine = w < n_items ? (n_items - w + DW - 1) / DW : 0;   // items of this wave
-    if (prefetched) {
-      // forced tile (item w) and the wave's candidate, both loaded earlier
+    auto load_compute = [&](int blk, int sub) {
+      TileBuf<D> X;
+      int x0, x1;
+      tokens(blk, sub, x0, x1);
+      tile_load<D>(kbase, vbase, row_bytes, x0, x1, X);
       __builtin_amdgcn_sched_barrier(0);
-      if (p_load) compute(p0, p1, P);
-      if (c_take) compute(c0, c1, C);
-    } else if (mine > 0) {
-      // items loaded now, at most two in flight, each load issued for an
-      // item the wave computes
-      TileBuf<D> A, B;
-      int a0, a1, b0, b1;
-      item(w, a0, a1);
-      load(a0, a1, A);
-      if (mine == 1) {
-        __builtin_amdgcn_sched_barrier(0);
-        compute(a0, a1, A);
-      } else {
-        item(w + DW, b0, b1);
-        load(b0, b1, B);
-        if (mine == 2) {
+      compute(x0, x1, X);
+    };
+    // (a) the forced items wu, wu + NW, ... (the first two loaded in phase 0)
+    const int n_items = k * n_sub;
+    const bool f0 = PF >= 1 && wu < n_items && wu < nf_items;
+    const bool f1 = PF >= 2 && wu + NW < n_items && wu + NW < nf_items;
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PF >= 1) {
+      if (f0) compute(p00, p01, P0);
+    }
+    if constexpr (PF >= 2) {
+      if (f1) compute(p10, p11, P1);
+    }
+    for (int j = wu + PF * NW; j < min(nf_items, n_items); j += NW) load_compute(forced_block(j / n_sub), j % n_sub);
+    // (b) the content blocks
+    if (use_pool) {
+      // content item i (rank i / n_sub) on wave (nf_items + i) % NW; this
+      // wave's first one (rank rho) was loaded before the count
+      for (int i = rho; i < KC * n_sub; i += NW) {
+        const int r = i / n_sub;
+        const uint64_t hit = __ballot(prank == r);
+        const int blk = key_index(readlane_u64(pk, (int)__builtin_ctzll(hit)));
+        if (i == rho && n_sub == 1 && blk == cablk) {
           __builtin_amdgcn_sched_barrier(0);
-          compute(a0, a1, A);
-          compute(b0, b1, B);
+          compute(ca0, ca1, CA);
         } else {
-          // A holds item j, B item j + DW
-          int j = w;
-          for (;;) {
-            __builtin_amdgcn_sched_barrier(0);
-            compute(a0, a1, A);
-            const bool more = j + 2 * DW < n_items;
-            if (more) {
-              item(j + 2 * DW, a0, a1);
-              load(a0, a1, A);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            compute(b0, b1, B);
-            if (!more) break;
-            j += 2 * DW;
-            if (j + DW >= n_items) {
-              __builtin_amdgcn_sched_barrier(0);
-              compute(a0, a1, A);
-              break;
-            }
-            item(j + DW, b0, b1);
-            load(b0, b1, B);
-          }
+          load_compute(blk, i % n_sub);
         }
       }
+    } else if (KC > 0 && fast) {
+      // this wave's own candidates that are ranked < KC
+      auto rank_of = [&](int c) { return c < kWave ? __builtin_amdgcn_readlane(cr0, c) : __builtin_amdgcn_readlane(cr1, c - kWave); };
+      auto block_of = [&](int c) { return key_index(c < kWave ? readlane_u64(ck0, c) : readlane_u64(ck1, c - kWave)); };
+      for (int j = 0; j < n_own; ++j) {
+        const int c = own0 + j;
+        if (rank_of(c) >= KC) continue;
+        const int blk = block_of(c);
+        for (int sub = 0; sub < n_sub; ++sub) load_compute(blk, sub);
+      }
+    } else if (KC > 0) {
+      // the general selection's list: content item i on wave i % NW
+      for (int i = wu; i < KC * n_sub; i += NW) load_compute(L.list[i / n_sub], i % n_sub);
     }
   }
   tile_finish(st);
-  if (w < DW && lane == 0) {
-    s_m[w] = st.m_h;
-    s_l[w] = st.l_h;
+  if (lane == 0) {
+    L.m[wu] = st.m_h;
+    L.l[wu] = st.l_h;
   }
-  if (w < DW && grp == 0) {
+  if (grp == 0) {
 #pragma unroll
-    for (int n = 0; n < NT16; ++n) s_acc[w][n * 16 + col] = st.acc[n][0];   // O[head 0][16n + col]
+    for (int n = 0; n < NT16; ++n) L.acc[wu][n * 16 + col] = st.acc[n][0];   // O[head 0][16n + col]
   }
   lds_barrier();
   for (int i = tid; i < D; i += NT) {
     float M = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < DW; ++ww) M = fmaxf(M, s_m[ww]);
-    float L = 0.f, O = 0.f;
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, L.m[ww]);
+    float Ls = 0.f, O = 0.f;
     if (M != -INFINITY) {
 #pragma unroll
-      for (int ww = 0; ww < DW; ++ww) {
-        const float f = s_m[ww] == -INFINITY ? 0.f : exp2f(s_m[ww] - M);
-        L += s_l[ww] * f;
-        O += s_acc[ww][i] * f;
+      for (int ww = 0; ww < NW; ++ww) {
+        const float f = L.m[ww] == -INFINITY ? 0.f : exp2f(L.m[ww] - M);
+        Ls += L.l[ww] * f;
+        O += L.acc[ww][i] * f;
       }
     }
-    store_elt(d.out, d.odt, oo + i, O / L);   // no block at all: 0/0 as the reference kernel
+    store_elt(d.out, d.odt, oo + i, O / Ls);   // no block at all: 0/0 as the reference kernel
   }
 }
 
-template <int KVDT, int D>
-hipError_t launch_fd(const FusedArgs& a, int max_blocks, hipStream_t s) {
+// Threads and scores per thread for a row bound: 256 threads up to 32
+// scores each (8192 blocks), then 512 threads with 32 (16384 blocks);
+// {0, 0}: not served.
+struct StepShape { int nt, ipt; };
+inline StepShape step_shape(int rows) {
+  for (int ipt = 4; ipt <= 32; ipt *= 2)
+    if (rows <= 256 * ipt) return {256, ipt};
+  if (rows <= 512 * 32) return {512, 32};
+  return {0, 0};
+}
+
+template <int KVDT, int D, int NT, int IPT>
+void launch_one(const FusedArgs& a, hipStream_t s) {
   const dim3 grid(a.s.Hq, a.s.B);
   const size_t dyn = (size_t)a.s.Hq * sizeof(double);
-  switch (fused_ipt(max_blocks)) {
-    case 4: hipLaunchKernelGGL((select_decode_kernel<KVDT, D, 4>), grid, dim3(kFusedThreads), dyn, s, a); break;
-    case 8: hipLaunchKernelGGL((select_decode_kernel<KVDT, D, 8>), grid, dim3(kFusedThreads), dyn, s, a); break;
-    case 16: hipLaunchKernelGGL((select_decode_kernel<KVDT, D, 16>), grid, dim3(kFusedThreads), dyn, s, a); break;
-    default: return hipErrorInvalidValue;
+  hipLaunchKernelGGL((select_decode_kernel<KVDT, D, NT, IPT>), grid, dim3(NT), dyn, s, a);
+}
+
+template <int KVDT, int D>
+hipError_t launch_fd(const FusedArgs& a, int rows, hipStream_t s) {
+  const StepShape sh = step_shape(rows);
+  if (sh.nt == 512) {
+    launch_one<KVDT, D, 512, 32>(a, s);
+  } else {
+    switch (sh.ipt) {
+      case 4: launch_one<KVDT, D, 256, 4>(a, s); break;
+      case 8: launch_one<KVDT, D, 256, 8>(a, s); break;
+      case 16: launch_one<KVDT, D, 256, 16>(a, s); break;
+      case 32: launch_one<KVDT, D, 256, 32>(a, s); break;
+      default: return hipErrorInvalidValue;
+    }
   }
   return hipGetLastError();
 }
 
 template <int KVDT>
-hipError_t launch_fk(const FusedArgs& a, int D, int max_blocks, hipStream_t s) {
+hipError_t launch_fk(const FusedArgs& a, int D, int rows, hipStream_t s) {
   switch (D) {
-    case 32: return launch_fd<KVDT, 32>(a, max_blocks, s);
-    case 64: return launch_fd<KVDT, 64>(a, max_blocks, s);
-    case 128: return launch_fd<KVDT, 128>(a, max_blocks, s);
+    case 32: return launch_fd<KVDT, 32>(a, rows, s);
+    case 64: return launch_fd<KVDT, 64>(a, rows, s);
+    case 128: return launch_fd<KVDT, 128>(a, rows, s);
     default: return hipErrorInvalidValue;
+  }
+}
+
+template <int NT>
+size_t step_lds(int D) {
+  switch (D) {
+    case 32: return sizeof(StepLds<NT, 32>);
+    case 64: return sizeof(StepLds<NT, 64>);
+    case 128: return sizeof(StepLds<NT, 128>);
+    default: return (size_t)-1;
   }
 }
 
 }  // namespace
 
-// The fused kernel serves head_dim <= 128 and up to 16 scores per thread (the
-// register budget of a 512-thread workgroup); other shapes take the
-// three-kernel path.
+// The fused kernel serves head_dim <= 128 and up to 16384 blocks; other
+// shapes take the three-kernel path.
 bool select_decode_supported(int D, int max_blocks, int table_width, int Hq, int sp, int parts_pitch) {
-  return D <= 128 && max_blocks <= kFusedThreads * 16 && table_width <= kSortCap &&
+  return D <= 128 && step_shape(max_blocks).nt > 0 && table_width <= kSortCap &&
          (int64_t)Hq * sp < (1ll << 31) && (int64_t)Hq * parts_pitch * kPartFloats < (1ll << 31);
 }
 
-template <int D>
-size_t fused_lds_d(int ipt) {
-  switch (ipt) {
-    case 4: return fused_static_lds<D, 4>();
-    case 8: return fused_static_lds<D, 8>();
-    case 16: return fused_static_lds<D, 16>();
-    default: return (size_t)-1;
-  }
-}
-
 size_t select_decode_lds(int D, int Hq, int max_blocks) {
-  const int ipt = fused_ipt(max_blocks);
-  size_t st = 0;
-  switch (D) {
-    case 32: st = fused_lds_d<32>(ipt); break;
-    case 64: st = fused_lds_d<64>(ipt); break;
-    case 128: st = fused_lds_d<128>(ipt); break;
-    default: return (size_t)-1;
-  }
-  return st == (size_t)-1 ? st : st + (size_t)Hq * sizeof(double);
+  const StepShape sh = step_shape(max_blocks);
+  const size_t st = sh.nt == 512 ? step_lds<512>(D) : step_lds<256>(D);
+  if (st == (size_t)-1) return st;
+  return st + (size_t)Hq * sizeof(double);
 }
 
 hipError_t launch_select_decode(const FusedArgs& a, int kvdt, int D, int max_blocks, hipStream_t s) {

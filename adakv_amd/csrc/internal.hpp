@@ -48,11 +48,11 @@ struct ScoreArgs {
   int minmax;                  // 1: rows are minmax summaries [max | min] of 2*head_dim elements
 };
 
-// Softmax record of a score workgroup's rows for one head (z = score /
-// temperature): m = max z, S = sum exp(z - m), T = sum exp(z - m) * (z - m),
-// then the sanitised content maxima of its 4 sub-chunks (-inf: none) and one
-// unused float.  8 floats (32 bytes).
-constexpr int kPartFloats = 8;
+// Record of a score workgroup's rows for one head (layout in select.hpp):
+// the softmax partial of z = score / temperature (m = max z, S = sum
+// exp(z - m), T = sum exp(z - m) * (z - m)) and the exact top two content
+// blocks of each of its 4 sub-chunks and a bound of the rest.  20 floats (80 bytes).
+constexpr int kPartFloats = 20;
 
 struct SelectArgs {
   const float* scores;

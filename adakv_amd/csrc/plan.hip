@@ -76,7 +76,7 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
                                                                   kPartFloats);
     const float4 r0 = rec[0], r1 = rec[1];
     pt = soft_merge(pt, SoftPart{r0.x, r0.y, r0.z});
-    const float mx[4] = {r0.w, r1.x, r1.y, r1.z};
+    const float mx[4] = {r1.x, r1.y, r1.z, r1.w};   // the sub-chunks' largest content scores
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (4 * c + i < NT) L.maxv[4 * c + i] = mx[i];

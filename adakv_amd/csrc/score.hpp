@@ -119,13 +119,18 @@ __device__ __forceinline__ void append_block(const ScoreArgs& a, int b, int kvh,
   }
 }
 
-// Softmax partial of a score workgroup's rows for one head, written by one
-// lane: m, S, T and the content maxima of the 4 sub-chunks (select.hpp).
+// Record of a score workgroup's rows for one head, written by one lane: the
+// softmax partial m, S, T and the top two content blocks of each of the 4
+// sub-chunks with a bound of the rest (layout in select.hpp).
 __device__ __forceinline__ void write_part(const ScoreArgs& a, int b, int h, int slot, float m, float S, float T,
-                                           float hi0, float hi1, float hi2, float hi3) {
+                                           const Top2 (&t)[4]) {
   float4* rec = reinterpret_cast<float4*>(a.parts + (((int64_t)b * a.Hq + h) * a.parts_pitch + slot) * kPartFloats);
-  rec[0] = make_float4(m, S, T, hi0);
-  rec[1] = make_float4(hi1, hi2, hi3, 0.f);
+  auto pk = [](const Top2& x) { return __uint_as_float(((uint32_t)x.r1 & 0xffffu) | ((uint32_t)x.r2 << 16)); };
+  rec[0] = make_float4(m, S, T, 0.f);
+  rec[1] = make_float4(t[0].v1, t[1].v1, t[2].v1, t[3].v1);
+  rec[2] = make_float4(t[0].v2, t[1].v2, t[2].v2, t[3].v2);
+  rec[3] = make_float4(t[0].v3, t[1].v3, t[2].v3, t[3].v3);
+  rec[4] = make_float4(pk(t[0]), pk(t[1]), pk(t[2]), pk(t[3]));
 }
 
 // fp32 centroids: one workgroup per chunk of CB blocks; every centroid row is
@@ -192,7 +197,8 @@ __device__ __forceinline__ void score_chunk_valu(const ScoreArgs& a, int b, int 
   const float tf = (float)fmax(a.cfg.temperature, 1e-6);
   for (int g = w; g < G; g += kNT / kWave) {
     float z[RL];
-    float m = -INFINITY, hi = -INFINITY;
+    float m = -INFINITY;
+    Top2 tp = top2_empty();
 #pragma unroll
     for (int k = 0; k < RL; ++k) {
       const int r = lane + k * kWave;
@@ -200,8 +206,9 @@ __device__ __forceinline__ void score_chunk_valu(const ScoreArgs& a, int b, int 
       const float x = ok ? s_sc[g][r] : 0.f;
       z[k] = ok ? (tf == 1.f ? x : __fdiv_rn(x, tf)) : -INFINITY;
       m = fmaxf(m, z[k]);
-      if (ok && row0 + r >= c_lo && row0 + r < c_hi) hi = fmaxf(hi, sanitize(x));
+      top2_push(tp, (ok && row0 + r >= c_lo && row0 + r < c_hi) ? sanitize(x) : -INFINITY, row0 + r);
     }
+    tp = top2_wave(tp);
     m = wave_allreduce(m, OpMax());
     float S = 0.f, T = 0.f;
     if (m != -INFINITY) {
@@ -216,8 +223,8 @@ __device__ __forceinline__ void score_chunk_valu(const ScoreArgs& a, int b, int 
     }
     S = wave_allreduce(S, OpAdd());
     T = wave_allreduce(T, OpAdd());
-    hi = wave_allreduce(hi, OpMax());
-    if (lane == 0) write_part(a, b, kvh * G + g, unit, m, S, T, hi, -INFINITY, -INFINITY, -INFINITY);
+    const Top2 t4[4] = {tp, top2_empty(), top2_empty(), top2_empty()};   // the chunk is one sub-chunk
+    if (lane == 0) write_part(a, b, kvh * G + g, unit, m, S, T, t4);
   }
 }
 
@@ -231,7 +238,7 @@ __device__ __forceinline__ void score_chunk_valu(const ScoreArgs& a, int b, int 
 // partials are merged through LDS into the workgroup's record.
 template <int CDT, int D, int GMAX, bool MM, int TPW>
 __device__ __forceinline__ void score_chunk_mfma(const ScoreArgs& a, int b, int kvh, int unit, int nb, int nrows,
-                                 float (*s_pm)[GMAX][4]) {
+                                 float (*s_pm)[GMAX][4], Top2 (*s_tp)[GMAX]) {
   static_assert(D % 32 == 0 && GMAX <= 16, "16x16 tiles over head_dim");
   constexpr int KS = D / 32;                // k-steps (16-byte loads per lane per tile)
   constexpr int QS = MM ? KS / 2 : KS;      // distinct q slices (a minmax row repeats q: max(q,0), min(q,0))
@@ -244,7 +251,8 @@ __device__ __forceinline__ void score_chunk_mfma(const ScoreArgs& a, int b, int 
   const int wrow0 = unit * NWV * RPW + w * RPW;
   if (unit * NWV * RPW >= nrows) return;    // uniform over the workgroup
   const bool wave_on = wrow0 < nrows;       // uniform over the wave
-  float m = -INFINITY, S = 0.f, T = 0.f, hi = -INFINITY;
+  float m = -INFINITY, S = 0.f, T = 0.f;
+  Top2 tp = top2_empty();
   if (wave_on) {
     // B fragments: lane (col, grp) holds q[head col][32s + 8grp .. +7] (columns
     // col >= G repeat the last head; their scores are never stored); for a
@@ -349,24 +357,29 @@ __device__ __forceinline__ void score_chunk_mfma(const ScoreArgs& a, int b, int 
     // the masked path.
     const bool full = wrow0 >= c_lo && wrow0 + RPW <= min(c_hi, nrows);
     float mx = -INFINITY;
+    // the exact top two content rows of the sub-chunk for head col: this
+    // lane's rows in increasing order, then the 4 lanes of the column
     if (full) {
 #pragma unroll
       for (int t = 0; t < TPW; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[t][i]);
-      hi = sanitize(mx);
+        for (int i = 0; i < 4; ++i) {
+          mx = fmaxf(mx, sc[t][i]);
+          top2_push(tp, sanitize(sc[t][i]), wrow0 + 16 * t + 4 * grp + i);
+        }
     } else {
-      // branch-free: content and validity are selects, empty rows contribute exp(-inf) = 0
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = wrow0 + 16 * t + 4 * grp + i;
           const bool cont = (r >= c_lo) & (r < c_hi) & (r < nrows);
-          hi = fmaxf(hi, cont ? sanitize(sc[t][i]) : -INFINITY);
+          top2_push(tp, cont ? sanitize(sc[t][i]) : -INFINITY, r);
         }
       }
     }
+    tp = top2_merge_lanes<16>(tp);
+    tp = top2_merge_lanes<32>(tp);
     if (tf != 1.f) {   // temperature: the correctly rounded division only when it is needed (uniform)
 #pragma unroll
       for (int t = 0; t < TPW; ++t)
@@ -400,11 +413,11 @@ __device__ __forceinline__ void score_chunk_mfma(const ScoreArgs& a, int b, int 
       }
     pr = swap16(S); S = pr.a + pr.b; pr = swap32(S); S = pr.a + pr.b;
     pr = swap16(T); T = pr.a + pr.b; pr = swap32(T); T = pr.a + pr.b;
-    pr = swap16(hi); hi = fmaxf(pr.a, pr.b); pr = swap32(hi); hi = fmaxf(pr.a, pr.b);
   }
   if (a.parts == nullptr) return;           // uniform
   if (grp == 0 && col < G) {
-    s_pm[w][col][0] = m; s_pm[w][col][1] = S; s_pm[w][col][2] = T; s_pm[w][col][3] = hi;
+    s_pm[w][col][0] = m; s_pm[w][col][1] = S; s_pm[w][col][2] = T;
+    s_tp[w][col] = tp;
   }
   __syncthreads();
   if (w == 0 && lane < G) {
@@ -424,8 +437,8 @@ __device__ __forceinline__ void score_chunk_mfma(const ScoreArgs& a, int b, int 
         }
       }
     }
-    write_part(a, b, kvh * G + lane, unit, M, SS, TT, s_pm[0][lane][3], s_pm[1][lane][3], s_pm[2][lane][3],
-               s_pm[3][lane][3]);
+    const Top2 t4[4] = {s_tp[0][lane], s_tp[1][lane], s_tp[2][lane], s_tp[3][lane]};
+    write_part(a, b, kvh * G + lane, unit, M, SS, TT, t4);
   }
 }
 
@@ -435,12 +448,14 @@ __device__ __forceinline__ void score_chunk_mfma(const ScoreArgs& a, int b, int 
 // then n_chunks workgroups per (sequence, KV head).
 template <int CDT, int D, int GMAX, bool MM, int TPW>
 __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
+  warm_kernargs<sizeof(ScoreArgs) + 8>();
   constexpr bool kMfma = CDT != ADAKV_F32;
   constexpr int CBV = (kNT / kWave) * (kWave / (D / Elt<CDT>::kPerVec)) * 4;   // VALU rows per workgroup
   __shared__ float s_q[GMAX][D];
   __shared__ float s_sc[kMfma ? 1 : GMAX * CBV];
   __shared__ float s_red[GMAX][kNT / kWave];
   __shared__ float s_pm[kNT / kWave][GMAX][4];
+  __shared__ Top2 s_tp[kNT / kWave][GMAX];
 
   int id = blockIdx.x;
   const bool app = id < a.n_app * a.Hkv * a.B;
@@ -458,7 +473,13 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
   // the same chunk indices of every sequence, and in a ragged batch (the high
   // chunks of short sequences empty) the CUs of the high chunks would idle.
   if (!app) unit = (unit + 8 * b) % a.n_chunks;
-  const int len = seq_len_of(a.seq_lens, a.uniform_len, b);
+  // uniform values kept in scalar registers (divisions expanded on the vector
+  // unit and a length loaded from memory would otherwise move every bound and
+  // address derived from them to the vector unit)
+  unit = __builtin_amdgcn_readfirstlane(unit);
+  kvh = __builtin_amdgcn_readfirstlane(kvh);
+  b = __builtin_amdgcn_readfirstlane(b);
+  const int len = __builtin_amdgcn_readfirstlane(seq_len_of(a.seq_lens, a.uniform_len, b));
   const int nb = len > 0 ? ceil_div(len, a.bs) : 0;
   const int first_app = a.n_new > 0 ? max(len - a.n_new, 0) / a.bs : nb;
   const int G = a.G;
@@ -471,7 +492,7 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
   }
   const int nrows = min(nb, first_app);     // appended blocks are scored by their own workgroups
   if constexpr (kMfma) {
-    score_chunk_mfma<CDT, D, GMAX, MM, TPW>(a, b, kvh, unit, nb, nrows, s_pm);
+    score_chunk_mfma<CDT, D, GMAX, MM, TPW>(a, b, kvh, unit, nb, nrows, s_pm, s_tp);
   } else {
     if (unit * CBV >= nrows) return;
     score_chunk_valu<CDT, D, GMAX, MM>(a, b, kvh, unit, nb, nrows, s_q, s_sc);

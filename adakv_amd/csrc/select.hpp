@@ -76,8 +76,16 @@ __device__ __forceinline__ int popcnt(M m) {
 // sum p log p = T / S - log S over the whole set.
 //
 // Record written by the score kernel per (sequence, q-head, score workgroup),
-// kPartFloats floats: m, S, T, then the content maxima of the workgroup's 4
-// sub-chunks (-inf: no content block in the sub-chunk), then one unused float.
+// kPartFloats = 20 floats in five 16-byte groups:
+//   [0..3]   m, S, T of the workgroup's rows, one unused float;
+//   [4..7]   the largest sanitised content score of each of its 4 sub-chunks
+//            (the rows of one wave; -inf: no content block);
+//   [8..11]  the second largest of each sub-chunk (-inf: fewer than two);
+//   [12..15] the third largest of each sub-chunk (-inf: fewer than three),
+//            which bounds every content score of the sub-chunk but the two;
+//   [16..19] the blocks holding the two, (first | second << 16) per
+//            sub-chunk (0xffff: none).
+// The two are exact in the selector's order (larger score, then lower block).
 struct SoftPart {
   float m, S, T;
 };
@@ -91,16 +99,17 @@ __device__ __forceinline__ SoftPart soft_merge(const SoftPart& x, const SoftPart
                   (x.m == -INFINITY ? 0.f : fx * fmaf(dx, x.S, x.T)) + (y.m == -INFINITY ? 0.f : fy * fmaf(dy, y.S, y.T))};
 }
 
-// Merge over aligned groups of N lanes (N = 16, 32 or 64): the max first,
-// then every lane rescales its sums to it once and the sums are added.
+// Merge over aligned groups of N lanes (N a power of two <= 64): the max
+// first, then every lane rescales its sums to it once and the sums are added.
 template <int N>
 __device__ __forceinline__ SoftPart soft_group_merge(SoftPart p) {
-  static_assert(N == 16 || N == 32 || N == 64, "row, half-wave or wave groups");
+  static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "aligned power-of-two lane groups");
+  if constexpr (N == 1) return p;
   float M = p.m;
-  M = fmaxf(M, dpp_mov<0xB1>(M));
-  M = fmaxf(M, dpp_mov<0x4E>(M));
-  M = fmaxf(M, dpp_mov<0x141>(M));
-  M = fmaxf(M, dpp_mov<0x140>(M));
+  if constexpr (N >= 2) M = fmaxf(M, dpp_mov<0xB1>(M));
+  if constexpr (N >= 4) M = fmaxf(M, dpp_mov<0x4E>(M));
+  if constexpr (N >= 8) M = fmaxf(M, dpp_mov<0x141>(M));
+  if constexpr (N >= 16) M = fmaxf(M, dpp_mov<0x140>(M));
   if constexpr (N >= 32) { const LanePair q = swap16(M); M = fmaxf(q.a, q.b); }
   if constexpr (N == 64) { const LanePair q = swap32(M); M = fmaxf(q.a, q.b); }
   float S = 0.f, T = 0.f;
@@ -110,6 +119,67 @@ __device__ __forceinline__ SoftPart soft_group_merge(SoftPart p) {
     T = f * fmaf(d, p.S, p.T);
   }
   return SoftPart{M, group_sum<N>(S), group_sum<N>(T)};
+}
+
+// ---- the exact top two of a set of (score, block) entries --------------------
+// Order of the selector (adakv/selector.py:44-52): larger score first, then the
+// lower block.  Empty entries are (-inf, 0xffff).  v3 bounds every entry of
+// the set outside the top two (the third largest score; -inf: none).
+struct Top2 {
+  float v1, v2, v3;
+  int r1, r2;
+};
+__device__ __forceinline__ Top2 top2_empty() { return Top2{-INFINITY, -INFINITY, -INFINITY, 0xffff, 0xffff}; }
+__device__ __forceinline__ bool entry_before(float va, int ra, float vb, int rb) {
+  return va > vb || (va == vb && ra < rb);
+}
+// Adds entry (x, r); r is above every block added before, so an equal score
+// added later ranks after the earlier one.
+__device__ __forceinline__ void top2_push(Top2& t, float x, int r) {
+  const bool c1 = x > t.v1, c2 = x > t.v2;   // c1 implies c2
+  t.v3 = c2 ? t.v2 : fmaxf(t.v3, x);
+  t.v2 = c1 ? t.v1 : (c2 ? x : t.v2);
+  t.r2 = c1 ? t.r1 : (c2 ? r : t.r2);
+  t.v1 = c1 ? x : t.v1;
+  t.r1 = c1 ? r : t.r1;
+}
+// The top two (and bound) of the union of two disjoint sets, each given by its
+// own (symmetric in its arguments).
+__device__ __forceinline__ Top2 top2_merge(const Top2& a, const Top2& b) {
+  const bool aw = entry_before(a.v1, a.r1, b.v1, b.r1);
+  const float lv = aw ? b.v1 : a.v1, sv = aw ? a.v2 : b.v2;   // loser's first, winner's second
+  const int lr = aw ? b.r1 : a.r1, sr = aw ? a.r2 : b.r2;
+  const bool lw = entry_before(lv, lr, sv, sr);
+  // outside the new top two: the other of (lv, sv), the loser's second, both bounds
+  const float rest = fmaxf(fmaxf(lw ? sv : lv, aw ? b.v2 : a.v2), fmaxf(a.v3, b.v3));
+  return Top2{aw ? a.v1 : b.v1, lw ? lv : sv, rest, aw ? a.r1 : b.r1, lw ? lr : sr};
+}
+// Merge with the lane across a 16-lane row (swap16) or wave half (swap32).
+template <int XOR>
+__device__ __forceinline__ Top2 top2_merge_lanes(const Top2& t) {
+  static_assert(XOR == 16 || XOR == 32, "row or half-wave partners");
+  auto sw = [](float x) { return XOR == 16 ? swap16(x) : swap32(x); };
+  const LanePair v1 = sw(t.v1), v2 = sw(t.v2), v3 = sw(t.v3), r1 = sw(__int_as_float(t.r1)),
+                 r2 = sw(__int_as_float(t.r2));
+  return top2_merge(Top2{v1.a, v2.a, v3.a, __float_as_int(r1.a), __float_as_int(r2.a)},
+                    Top2{v1.b, v2.b, v3.b, __float_as_int(r1.b), __float_as_int(r2.b)});
+}
+// Merge with a DPP partner within 16 lanes (quad_perm / mirror controls, which
+// pair lanes symmetrically).
+template <int CTRL>
+__device__ __forceinline__ Top2 top2_merge_dpp(const Top2& t) {
+  const Top2 o{dpp_mov<CTRL>(t.v1), dpp_mov<CTRL>(t.v2), dpp_mov<CTRL>(t.v3),
+               __float_as_int(dpp_mov<CTRL>(__int_as_float(t.r1))), __float_as_int(dpp_mov<CTRL>(__int_as_float(t.r2)))};
+  return top2_merge(t, o);
+}
+// Over the whole wave (every lane receives the result).
+__device__ __forceinline__ Top2 top2_wave(Top2 t) {
+  t = top2_merge_dpp<0xB1>(t);
+  t = top2_merge_dpp<0x4E>(t);
+  t = top2_merge_dpp<0x141>(t);
+  t = top2_merge_dpp<0x140>(t);
+  t = top2_merge_lanes<16>(t);
+  return top2_merge_lanes<32>(t);
 }
 
 // Normalised entropy weight (adakv/budget.py:33-37) from the merged partial of
