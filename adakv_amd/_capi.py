@@ -29,7 +29,7 @@ NOALLOC_SCRATCH_BYTES = 16 << 20
 ADAKV_F32, ADAKV_F16, ADAKV_BF16 = 0, 1, 2
 POLICY_FIXED, POLICY_ADAPTIVE, POLICY_NUCLEUS = 0, 1, 2
 SUMMARY_CENTROID, SUMMARY_MINMAX = 0, 1
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class Geometry(ctypes.Structure):
@@ -93,6 +93,8 @@ SIGNATURES = {
     "adakv_decode_fused": (ctypes.c_int, [P(Geometry), P(Query), P(KV), P(Centroid), c_void_p,
                                           P(Budget), P(Selection), c_int32, ctypes.c_float,
                                           P(Output), c_void_p, ctypes.c_size_t, c_void_p]),
+    "adakv_decode_fused_scan": (ctypes.c_int, [P(Geometry), P(Query), P(KV), P(Centroid), c_void_p,
+                                               P(Budget), c_int32, c_void_p, ctypes.c_size_t, c_void_p]),
     "adakv_decode_fused_noalloc": (ctypes.c_int, [P(Geometry), P(Query), P(KV), P(Centroid), c_void_p,
                                                   P(Budget), P(Selection), c_int32, ctypes.c_float,
                                                   P(Output), c_void_p]),

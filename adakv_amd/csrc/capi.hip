@@ -444,7 +444,7 @@ int decode_fused_impl(const adakv_geometry_t* g, const adakv_query_t* q, const a
   if (kv->dtype != ADAKV_F32 && q->dtype == kv->dtype && aligned16(q->data) && q->stride_b % 8 == 0 &&
       q->stride_h % 8 == 0 &&
       select_decode_supported(g->head_dim, rows_bound(g), T, g->n_q_heads, L.sp, L.parts_pitch) &&
-      select_decode_lds(g->head_dim, g->n_q_heads, rows_bound(g)) <= max_lds_per_block()) {
+      select_decode_lds(g->head_dim, g->n_q_heads, rows_bound(g), p->avg_budget) <= max_lds_per_block()) {
     FusedArgs fa{};
     if ((st = run_scores(g, q, c, kv, append_new, seq_lens, p, table, Tl, w, s, &fa.s))) return st;
     if (p->policy == ADAKV_POLICY_NUCLEUS && launch_nucleus(fa.s, rows_bound(g), s) != hipSuccess)
@@ -559,6 +559,24 @@ int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const 
                        void* stream) {
   return decode_fused_impl(g, q, kv, c, seq_lens, p, sel, append_new, sm_scale, out, ws, ws_bytes, stream,
                            false);
+}
+
+int adakv_decode_fused_scan(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
+                            const adakv_centroid_t* c, const int32_t* seq_lens, const adakv_budget_t* p,
+                            int32_t append_new, void* ws, size_t ws_bytes, void* stream) {
+  int st;
+  if ((st = check_geometry(g)) || (st = check_q(q)) || (st = check_kv(g, kv, true)) ||
+      (st = check_centroid(g, c)) || (st = check_budget(p)))
+    return st;
+  if (append_new < 0 || append_new > g->max_seq_len) return ADAKV_ERR_VALUE;
+  const int T = table_width_of(g, p);
+  if ((st = check_ws(g, T, ws, ws_bytes))) return st;
+  if (append_new > 0 && !centroid_pair_ok(kv->dtype, c)) return ADAKV_ERR_DTYPE;
+  char* w = reinterpret_cast<char*>(ws);
+  const WorkspaceLayout L = workspace_layout(*g, T);
+  SelectArgs se;
+  return run_scores(g, q, c, kv, append_new, seq_lens, p, reinterpret_cast<int32_t*>(w + L.table), T, w,
+                    (hipStream_t)stream, &se);
 }
 
 int adakv_decode_fused_noalloc(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,

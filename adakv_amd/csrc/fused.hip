@@ -390,9 +390,10 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
     t_hi = min(min(blk * a.bs + a.bs, len), t0 + 16);
   };
   auto forced_block = [&](int e) { return e < bb.sink ? e : local_lo + (e - bb.sink); };
-  // PF forced items per wave are prefetched (none with 512 threads: 8 waves
-  // already cover the forced items, and two waves per SIMD halve the register file)
-  constexpr int PF = NT == 256 ? 2 : 0;
+  // PF forced items per wave are prefetched (one with 512 threads: 8 waves
+  // cover the usual sink + local count, and two waves per SIMD halve the
+  // register file)
+  constexpr int PF = NT == 256 ? 2 : 1;
   TileBuf<D> P0, P1;
   int p00 = 0, p01 = 1, p10 = 0, p11 = 1;
   if constexpr (PF >= 1) {
@@ -559,12 +560,11 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
     if (use_pool && wu == 0 && prank < KC) trow[nf + prank] = key_index(pk);
   }
   // full path: every score of the head (thread t owns blocks [t*IPT,
-  // (t+1)*IPT)); its own candidates (ck, cr) or the general selection's list
+  // (t+1)*IPT)); the ranked candidates (ck, cr) or the general selection's list
   constexpr int kBig = 1 << 30;
   bool fast = false;
   uint64_t ck0 = 0, ck1 = 0;
   int cr0 = kBig, cr1 = kBig;
-  int n_own = 0, own0 = 0;
   if (KC > 0 && !use_pool) {
     const int base = tid * IPT;
     float v[IPT];
@@ -648,9 +648,6 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
         n_cand += max(wn[ww], 0);
       }
       fast = !over && n_cand <= kCap;
-      n_own = max(wn[wu], 0);
-#pragma unroll
-      for (int ww = 0; ww < NW; ++ww) own0 += ww < wu ? max(wn[ww], 0) : 0;
       if (fast) {
         auto fetch = [&](int idx) -> uint64_t {   // candidate idx of the concatenated lists
           int src = 0;
@@ -719,34 +716,57 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
       if (f1) compute(p10, p11, P1);
     }
     for (int j = wu + PF * NW; j < min(nf_items, n_items); j += NW) load_compute(forced_block(j / n_sub), j % n_sub);
-    // (b) the content blocks
-    if (use_pool) {
-      // content item i (rank i / n_sub) on wave (nf_items + i) % NW; this
-      // wave's first one (rank rho) was loaded before the count
-      for (int i = rho; i < KC * n_sub; i += NW) {
-        const int r = i / n_sub;
+    // (b) the content blocks: item i (sub-tile i % n_sub of the block of rank
+    // i / n_sub) on wave (nf_items + i) % NW, so this wave's are rho, rho + NW,
+    // ...; the block of a rank is a ballot away in the pool and fast paths
+    // (every wave holds all ranked candidates), in LDS for the general one
+    auto block_of = [&](int r) -> int {
+      if (use_pool) {
         const uint64_t hit = __ballot(prank == r);
-        const int blk = key_index(readlane_u64(pk, (int)__builtin_ctzll(hit)));
-        if (i == rho && n_sub == 1 && blk == cablk) {
+        return key_index(readlane_u64(pk, hit ? (int)__builtin_ctzll(hit) : 0));
+      }
+      if (fast) {
+        const uint64_t h0 = __ballot(cr0 == r);
+        if (h0) return key_index(readlane_u64(ck0, (int)__builtin_ctzll(h0)));
+        const uint64_t h1 = __ballot(cr1 == r);
+        return key_index(readlane_u64(ck1, h1 ? (int)__builtin_ctzll(h1) : 0));
+      }
+      return L.list[r];
+    };
+    // up to three tiles in flight: item n + 3's load is issued right after
+    // item n's compute; the first item may be the tile prefetched before the
+    // count
+    auto fetch = [&](int it, TileBuf<D>& T, int& t0, int& t1) {
+      const int blk = block_of(it / n_sub);
+      if (it == rho && n_sub == 1 && blk == cablk) {
+        T = CA;
+        t0 = ca0;
+        t1 = ca1;
+      } else {
+        tokens(blk, it % n_sub, t0, t1);
+        tile_load<D>(kbase, vbase, row_bytes, t0, t1, T);
+      }
+    };
+    constexpr int kRing = 3;
+    const int n_ci = KC * n_sub;
+    TileBuf<D> R[kRing];
+    int r0[kRing], r1[kRing];
+#pragma unroll
+    for (int u = 0; u < kRing; ++u) {
+      r0[u] = 0;
+      r1[u] = 1;
+      if (rho + u * NW < n_ci) fetch(rho + u * NW, R[u], r0[u], r1[u]);
+    }
+    for (int base = rho; base < n_ci; base += kRing * NW) {
+#pragma unroll
+      for (int u = 0; u < kRing; ++u) {
+        const int it = base + u * NW;
+        if (it < n_ci) {
           __builtin_amdgcn_sched_barrier(0);
-          compute(ca0, ca1, CA);
-        } else {
-          load_compute(blk, i % n_sub);
+          compute(r0[u], r1[u], R[u]);
+          if (it + kRing * NW < n_ci) fetch(it + kRing * NW, R[u], r0[u], r1[u]);
         }
       }
-    } else if (KC > 0 && fast) {
-      // this wave's own candidates that are ranked < KC
-      auto rank_of = [&](int c) { return c < kWave ? __builtin_amdgcn_readlane(cr0, c) : __builtin_amdgcn_readlane(cr1, c - kWave); };
-      auto block_of = [&](int c) { return key_index(c < kWave ? readlane_u64(ck0, c) : readlane_u64(ck1, c - kWave)); };
-      for (int j = 0; j < n_own; ++j) {
-        const int c = own0 + j;
-        if (rank_of(c) >= KC) continue;
-        const int blk = block_of(c);
-        for (int sub = 0; sub < n_sub; ++sub) load_compute(blk, sub);
-      }
-    } else if (KC > 0) {
-      // the general selection's list: content item i on wave i % NW
-      for (int i = wu; i < KC * n_sub; i += NW) load_compute(L.list[i / n_sub], i % n_sub);
     }
   }
   tile_finish(st);
@@ -776,13 +796,20 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   }
 }
 
-// Threads and scores per thread for a row bound: 256 threads up to 32
-// scores each (8192 blocks), then 512 threads with 32 (16384 blocks);
-// {0, 0}: not served.
+// Threads and scores per thread for a row bound and the budget's mean count
+// avg: 256 threads up to 16 scores each (4096 blocks); up to 8192 blocks,
+// 256 threads with 32 when avg <= kWideBudget (a few content tiles per head:
+// four waves, fewer barrier partners), else 512 threads with 16 (eight waves
+// halve a large budget's serial decode); 512 threads with 32 up to 16384
+// blocks; {0, 0}: not served.  Measured at 128K: avg 8, 17.9 us with 256
+// threads against 18.7 with 512; avg 32, 40.6 against 30.2.
+constexpr double kWideBudget = 12.0;
 struct StepShape { int nt, ipt; };
-inline StepShape step_shape(int rows) {
-  for (int ipt = 4; ipt <= 32; ipt *= 2)
+inline StepShape step_shape(int rows, double avg) {
+  for (int ipt = 4; ipt <= 16; ipt *= 2)
     if (rows <= 256 * ipt) return {256, ipt};
+  if (rows <= 256 * 32 && avg <= kWideBudget) return {256, 32};
+  if (rows <= 512 * 16) return {512, 16};
   if (rows <= 512 * 32) return {512, 32};
   return {0, 0};
 }
@@ -796,9 +823,10 @@ void launch_one(const FusedArgs& a, hipStream_t s) {
 
 template <int KVDT, int D>
 hipError_t launch_fd(const FusedArgs& a, int rows, hipStream_t s) {
-  const StepShape sh = step_shape(rows);
+  const StepShape sh = step_shape(rows, a.s.cfg.avg);
   if (sh.nt == 512) {
-    launch_one<KVDT, D, 512, 32>(a, s);
+    if (sh.ipt == 16) launch_one<KVDT, D, 512, 16>(a, s);
+    else launch_one<KVDT, D, 512, 32>(a, s);
   } else {
     switch (sh.ipt) {
       case 4: launch_one<KVDT, D, 256, 4>(a, s); break;
@@ -836,12 +864,12 @@ size_t step_lds(int D) {
 // The fused kernel serves head_dim <= 128 and up to 16384 blocks; other
 // shapes take the three-kernel path.
 bool select_decode_supported(int D, int max_blocks, int table_width, int Hq, int sp, int parts_pitch) {
-  return D <= 128 && step_shape(max_blocks).nt > 0 && table_width <= kSortCap &&
+  return D <= 128 && step_shape(max_blocks, 0.0).nt > 0 && table_width <= kSortCap &&
          (int64_t)Hq * sp < (1ll << 31) && (int64_t)Hq * parts_pitch * kPartFloats < (1ll << 31);
 }
 
-size_t select_decode_lds(int D, int Hq, int max_blocks) {
-  const StepShape sh = step_shape(max_blocks);
+size_t select_decode_lds(int D, int Hq, int max_blocks, double avg) {
+  const StepShape sh = step_shape(max_blocks, avg);
   const size_t st = sh.nt == 512 ? step_lds<512>(D) : step_lds<256>(D);
   if (st == (size_t)-1) return st;
   return st + (size_t)Hq * sizeof(double);

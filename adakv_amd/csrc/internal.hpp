@@ -161,7 +161,7 @@ hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 // Fused selection + decode: whether it serves a shape, its LDS bytes (static
 // + dynamic) for a head_dim and q-head count, and the launcher.
 bool select_decode_supported(int D, int max_blocks, int table_width, int Hq, int sp, int parts_pitch);
-size_t select_decode_lds(int D, int Hq, int max_blocks);
+size_t select_decode_lds(int D, int Hq, int max_blocks, double avg);
 hipError_t launch_select_decode(const FusedArgs& a, int kvdt, int D, int max_blocks, hipStream_t s);
 
 }  // namespace adakv

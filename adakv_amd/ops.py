@@ -340,6 +340,27 @@ def decode_fused(q, k, v, centroid, block_size: int, budget: BudgetParams, seq_l
     return out
 
 
+def decode_fused_scan(q, k, v, centroid, block_size: int, budget: BudgetParams, seq_lens=None,
+                      append_new: int = 0, estimator: str | None = None):
+    """The first of decode_fused's two launches, alone and as the step issues
+    it: summary append, block scores and their softmax records (left in the
+    workspace).  For timing the step's launches separately."""
+    dev = _on_device(q, k, v, centroid, seq_lens)
+    B, Hq, D = q.shape
+    _, Hkv, S, _ = k.shape
+    g = geometry(B, Hq, Hkv, D, block_size, S, centroid.shape[2])
+    cb = budget.to_c()
+    T = C.load().adakv_table_width(ctypes.byref(g), ctypes.byref(cb))
+    if T < 1:
+        C.check(C.ADAKV_ERR_SHAPE, "decode_fused_scan")
+    ws = workspace(dev, C.load().adakv_workspace_bytes(ctypes.byref(g), T))
+    C.check(C.load().adakv_decode_fused_scan(ctypes.byref(g), ctypes.byref(_q(q)), ctypes.byref(_kv(k, v)),
+                                             ctypes.byref(_centroid(centroid, D, estimator)),
+                                             _ptr(_seq_lens(seq_lens, dev)), ctypes.byref(cb), int(append_new),
+                                             _ptr(ws), ws.numel(), _stream(dev)),
+            "decode_fused_scan")
+
+
 def dense_decode(q, k, v, sm_scale=None, seq_lens=None, out=None):
     """Dense split-K flash-decode over every token (bench_decode_latency.py:40-53)."""
     dev = _on_device(q, k, v, seq_lens, out)

@@ -12,12 +12,15 @@ token, block scores, budget + selection, sparse split-K decode and merge
 (adakv_decode_fused).  Steps cycle over ``--layers`` independent layers'
 K/V/centroid buffers (32 by default: 16 GiB of K/V, 512 MiB of centroids,
 more than the 256 MB MALL) so every step reads HBM.  Launches are captured in
-a HIP graph (one graph = one pass over the layers) to take host overhead out.
+a HIP graph to take host overhead out: exactly --warmup untimed layer-steps,
+then exactly --steps timed ones.
 
 Prints one JSON line: value = microseconds per layer (lower is better), the
 achieved HBM GB/s on the algorithmic bytes of the op, the dense HIP
-flash-decode time at the same context, the roofline of the dominant kernel
-(the centroid scan) timed with HIP events, and the CPU oracle timed on one
+flash-decode time at the same context, the rooflines of the step's two
+launches (the scan launch timed alone with HIP events exactly as the step
+issues it; the select + decode launch as the rest of the step), and the CPU
+oracle timed on one
 layer of the same workload on this host.  ``cells`` holds the other methods of
 the reference's decode-latency table (benchmarks/efficiency/
 bench_decode_latency.py:11-19) on the same layers at the same avg_budget:
@@ -50,7 +53,7 @@ def log(msg: str) -> None:
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=640, help="timed layer-steps (rounded up to a multiple of --layers)")
+    ap.add_argument("--steps", type=int, default=640, help="timed layer-steps of the headline (exactly)")
     ap.add_argument("--warmup", type=int, default=64, help="untimed layer-steps")
     ap.add_argument("--ctx", type=int, default=131072)
     ap.add_argument("--avg-budget", type=float, default=8)
@@ -152,6 +155,11 @@ class Workload:
     def scores(self, l, buf):
         self.ops.block_scores(self.q[l], self.c[l], self.BS, seq_len=self.S, out=buf)
 
+    def scan(self, l):
+        """The step's first launch alone, as the step issues it."""
+        self.ops.decode_fused_scan(self.q[l], self.k[l], self.v[l], self.c[l], self.BS, self.budget,
+                                   append_new=1)
+
 
 def capture(torch, fn, layers, stream):
     """One HIP graph holding fn(0..layers-1), after a warm pass on the capture stream."""
@@ -165,6 +173,39 @@ def capture(torch, fn, layers, stream):
             fn(l)
     torch.cuda.synchronize()
     return g
+
+
+def capture_steps(torch, fn, n, layers, stream):
+    """One HIP graph of exactly n layer-steps fn(i % layers), i < n (the
+    caller has run fn eagerly on `stream` once, so nothing allocates inside)."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(n):
+            fn(i % layers)
+    torch.cuda.synchronize()
+    return g
+
+
+def time_exact(torch, fn, steps, warmup, layers, stream):
+    """Exactly `warmup` untimed layer-steps, then exactly `steps` timed ones
+    (one graph replay bracketed by synchronisations, HIP events on the
+    current stream).  The warm-up is an eager pass over the first
+    min(warmup, layers) layers (it also allocates the workspace), then a
+    graph of the rest.  Returns (ms, wall ms) of the timed steps."""
+    eager = max(1, min(warmup, layers))
+    with torch.cuda.stream(stream):
+        for i in range(eager):
+            fn(i % layers)
+    torch.cuda.synchronize()
+    g = capture_steps(torch, fn, steps, layers, stream)
+    if warmup > eager:
+        gw = capture_steps(torch, fn, warmup - eager, layers, stream)
+        gw.replay()
+        torch.cuda.synchronize()
+        del gw
+    ms, wall = time_graph(torch, g, 1, 0)
+    del g
+    return ms, wall
 
 
 def time_graph(torch, g, replays, warm):
@@ -209,6 +250,20 @@ def selection_bytes(torch, ops, w: Workload):
                 total=b_cent + b_kv + b_q + b_out + b_meta, union_blocks_per_layer=u)
 
 
+def scan_bytes(w: Workload):
+    """Algorithmic bytes of the step's scan launch at this shape: every
+    centroid row and q read, the fp32 scores and the 80-byte softmax records
+    (one per q-head and 256-row workgroup) written, and the centroid append
+    of the newest token's block (its 16 K rows read, its row and its scores
+    written)."""
+    e = 2
+    n_rec = w.Hq * ((w.nb + 255) // 256)
+    parts = dict(centroid=w.Hkv * w.nb * w.D * e, q=w.Hq * w.D * e, scores=w.Hq * w.nb * 4,
+                 records=n_rec * 80, append=w.Hkv * (w.BS * w.D * e + w.D * e) + w.Hq * 4)
+    parts["total"] = sum(parts.values())
+    return parts
+
+
 def ragged_batch(torch, ops, stream, seed, layers=16):
     """8 sequences with lengths uniform in [16K, 128K] (fixed
     seed), 32 q / 8 KV heads, head_dim 128, bf16, block_size 16, avg_budget 16;
@@ -246,13 +301,43 @@ def ragged_batch(torch, ops, stream, seed, layers=16):
     ms2, _ = time_graph(torch, g2, 3, 1)
     a_us, d_us = ms1 * 1e3 / (10 * layers), ms2 * 1e3 / (3 * layers)
     kv_dense = int(lens.sum()) * Hkv * D * 2 * 2
-    log(f"ragged batch (config 4, lengths {lens.tolist()}): adakv {a_us:.2f} us/step, dense {d_us:.2f} us/step")
+    # AdaKV's algorithmic bytes per step, from each layer's own selection:
+    # every sequence's centroid rows, each (sequence, KV head)'s union of
+    # selected blocks (K and V), q and out, the tables and counts
+    G = Hq // Hkv
+    nbs = [(int(n) + BS - 1) // BS for n in lens.tolist()]
+    b_cent = sum(nbs) * Hkv * D * 2
+    unions = []
+    for l in range(layers):
+        q, k, v, c, _ = L[l]
+        _, table, sel = ops.decode_fused(q, k, v, c, BS, budget, seq_lens=sl, return_selection=True)
+        t, n = table.cpu(), sel.cpu()
+        u = 0
+        for b in range(B):
+            for g in range(Hkv):
+                s = set()
+                for h in range(g * G, (g + 1) * G):
+                    s.update(t[b, h, : int(n[b, h])].tolist())
+                u += len(s)
+        unions.append(u)
+    u = sum(unions) / len(unions)
+    b_kv = u * BS * D * 2 * 2
+    b_qo = 2 * B * Hq * D * 2
+    b_meta = B * Hq * (table.shape[2] + 1) * 4 * 2
+    total = b_cent + b_kv + b_qo + b_meta
+    gbps = total / (a_us * 1e-6) / 1e9
+    log(f"ragged batch (config 4, lengths {lens.tolist()}): adakv {a_us:.2f} us/step ({gbps:.0f} GB/s), "
+        f"dense {d_us:.2f} us/step")
     del g1, g2, L
     torch.cuda.empty_cache()
     return {"config": "BASELINE config 4: 8 sequences, lengths uniform in [16K, 128K], avg_budget 16",
             "lengths": lens.tolist(), "layers_rotated": layers, "adakv_us_per_layer_step": round(a_us, 2),
             "dense_us_per_layer_step": round(d_us, 2), "speedup": round(d_us / a_us, 2),
-            "dense_GBps": round(kv_dense / (d_us * 1e-6) / 1e9, 1)}
+            "bytes_per_step": int(total), "centroid_bytes_per_step": int(b_cent),
+            "kv_bytes_per_step": int(b_kv), "union_blocks_per_step": round(u, 1),
+            "achieved_GBps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4),
+            "dense_GBps": round(kv_dense / (d_us * 1e-6) / 1e9, 1),
+            "dense_frac": round(kv_dense / (d_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
 
 
 def stream_copy_gbps(torch, nbytes: int = 1 << 30, reps: int = 10) -> float:
@@ -274,16 +359,19 @@ def stream_copy_gbps(torch, nbytes: int = 1 << 30, reps: int = 10) -> float:
 
 
 def profiled_traffic(path: str):
-    """HBM bytes per launch of the centroid scan, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary (calibrated against a plain copy); None if absent."""
+    """HBM bytes per launch of the step's kernels, {kernel: bytes}, from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (calibrated against a
+    plain copy; lines `traffic_bytes_per_launch[kernel]: bytes`); None if absent."""
+    out = {}
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1])
+                if line.startswith("traffic_bytes_per_launch["):
+                    name, val = line.split("]:", 1)
+                    out[name[len("traffic_bytes_per_launch["):]] = int(val)
     except OSError:
         pass
-    return None
+    return out or None
 
 
 def cpu_baseline(torch, w: Workload, budget_s: float):
@@ -553,28 +641,34 @@ def main():
     log(f"device {torch.cuda.get_device_name(0)}; building {args.layers} layers at ctx {args.ctx}")
     w = Workload(torch, ops, args.ctx, args.layers, args.avg_budget, args.seed)
     L = w.L
-    replays = max(1, math.ceil(args.steps / L))
-    warm = max(1, math.ceil(args.warmup / L))
-    steps = replays * L
+    steps, warmup = max(1, args.steps), max(0, args.warmup)
+    # the other legs keep one graph per pass over the layers
+    replays = max(1, math.ceil(steps / L))
+    warm = max(1, math.ceil(warmup / L))
+    cell_steps = replays * L
     stream = torch.cuda.Stream()
 
-    log("capturing the decode graph")
-    g_step = capture(torch, w.step, L, stream)
-    ms, wall = time_graph(torch, g_step, replays, warm)
+    log(f"timing {steps} layer-steps after {warmup} untimed ones")
+    ms, wall = time_exact(torch, w.step, steps, warmup, L, stream)
     us_layer = ms * 1e3 / steps
     log(f"adakv fused: {us_layer:.2f} us/layer (events), wall {wall * 1e3 / steps:.2f} us/layer")
 
     nbytes = selection_bytes(torch, ops, w)
     gbps = nbytes["total"] / (us_layer * 1e-6) / 1e9
 
-    # dominant kernel: the centroid scan, alone, over the same rotated layers
-    sbuf = torch.zeros(1, w.Hq, w.c[0].shape[2], device="cuda", dtype=torch.float32)
-    g_sc = capture(torch, lambda l: w.scores(l, sbuf), L, stream)
-    ms_sc, _ = time_graph(torch, g_sc, replays, warm)
+    # the step's two launches: the scan launch alone, exactly as the step
+    # issues it (append + scores + softmax records), the same number of
+    # times over the same layers; the select + decode launch is the rest
+    ms_sc, _ = time_exact(torch, w.scan, steps, warmup, L, stream)
     us_sc = ms_sc * 1e3 / steps
-    sc_bytes = nbytes["centroid"] + nbytes["q"] + w.Hq * w.nb * 4      # centroids + q read, scores written
-    sc_gbps = sc_bytes / (us_sc * 1e-6) / 1e9
-    log(f"centroid scan: {us_sc:.2f} us/launch, {sc_gbps:.0f} GB/s")
+    sc_bytes = scan_bytes(w)
+    sc_gbps = sc_bytes["total"] / (us_sc * 1e-6) / 1e9
+    log(f"scan launch: {us_sc:.2f} us/launch, {sc_gbps:.0f} GB/s")
+    us_sd = max(us_layer - us_sc, 1e-3)
+    sbuf = torch.zeros(1, w.Hq, w.c[0].shape[2], device="cuda", dtype=torch.float32)   # the minmax scan leg's scores
+    sd_bytes = nbytes["kv"] + nbytes["q"] + nbytes["out"] + nbytes["meta"] + sc_bytes["records"]
+    sd_gbps = sd_bytes / (us_sd * 1e-6) / 1e9
+    log(f"select + decode launch (step - scan): {us_sd:.2f} us, {sd_gbps:.0f} GB/s")
 
     copy_gbps = stream_copy_gbps(torch)
     log(f"stream copy: {copy_gbps:.0f} GB/s")
@@ -601,7 +695,7 @@ def main():
                                    ("streaming", w.streaming, None, "fixed")):
             g_c = capture(torch, fn, L, stream)
             ms_c, _ = time_graph(torch, g_c, replays, warm)
-            us_c = ms_c * 1e3 / steps
+            us_c = ms_c * 1e3 / cell_steps
             summ = w.m[0] if est == "minmax" else w.c[0] if est == "centroid" else None
             cells[name] = {"us_per_layer": round(us_c, 3), "estimator": est, "budget_policy": pol,
                            "summary_bytes_per_layer": 0 if summ is None else int(summ[:, :, : w.nb].numel() * 2)}
@@ -609,7 +703,7 @@ def main():
             del g_c
         g_ms = capture(torch, lambda l: w.minmax_scores(l, sbuf), L, stream)
         ms_ms, _ = time_graph(torch, g_ms, replays, warm)
-        us_ms = ms_ms * 1e3 / steps
+        us_ms = ms_ms * 1e3 / cell_steps
         ms_bytes = 2 * nbytes["centroid"] + nbytes["q"] + w.Hq * w.nb * 4
         cells["quest"]["scan_us"] = round(us_ms, 3)
         cells["quest"]["scan_GBps"] = round(ms_bytes / (us_ms * 1e-6) / 1e9, 1)
@@ -627,7 +721,7 @@ def main():
         w.budget = ops.BudgetParams(avg_budget=32)
         g32 = capture(torch, w.step, L, stream)
         ms32, _ = time_graph(torch, g32, replays, warm)
-        us32 = ms32 * 1e3 / steps
+        us32 = ms32 * 1e3 / cell_steps
         nb32 = selection_bytes(torch, ops, w)
         w.budget = b8
         avg32 = {"avg_budget": 32, "us_per_layer": round(us32, 3), "bytes_per_layer": int(nb32["total"]),
@@ -677,7 +771,7 @@ def main():
 
     res = {
         "metric": METRIC, "value": round(us_layer, 3), "unit": "us/layer", "n_gpus": 1,
-        "steps": steps, "warmup": warm * L, "ms_per_step": round(us_layer / 1e3, 6),
+        "steps": steps, "warmup": warmup, "ms_per_step": round(us_layer / 1e3, 6),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "llama3.1-8b attention layer decode, ctx 131072, avg_budget 8 (BASELINE config 3)",
@@ -692,12 +786,20 @@ def main():
         "dense_us_per_layer": None if dense_us is None else round(dense_us, 2),
         "speedup_vs_dense": None if dense_us is None else round(dense_us / us_layer, 2),
         "stream_copy_GBps": round(copy_gbps, 1),
-        "roofline": {"kernel": "score_kernel (centroid scan)", "bound": "hbm",
-                     "achieved": round(sc_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+        "roofline": {"kernel": "score_kernel (the step's scan launch: append + scores + records)",
+                     "bound": "hbm", "achieved": round(sc_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(sc_gbps / PEAK_HBM_GBPS, 4),
-                     "traffic": traffic if (traffic and args.ctx == 131072 and L == 32) else None,
-                     "launch_us": round(us_sc, 3), "bytes_per_launch": int(sc_bytes),
+                     "traffic": traffic.get("score_kernel") if (traffic and args.ctx == 131072 and L == 32) else None,
+                     "launch_us": round(us_sc, 3), "bytes_per_launch": int(sc_bytes["total"]),
+                     "bytes": {k: int(v) for k, v in sc_bytes.items()},
                      "frac_of_stream_copy": round(sc_gbps / copy_gbps, 4)},
+        "roofline_select_decode": {"kernel": "select_decode_kernel (budget + selection + decode), timed as "
+                                             "the step minus the scan launch (includes the launch gap)",
+                                   "bound": "hbm", "achieved": round(sd_gbps, 1), "peak": PEAK_HBM_GBPS,
+                                   "unit": "GB/s", "frac": round(sd_gbps / PEAK_HBM_GBPS, 4),
+                                   "traffic": traffic.get("select_decode_kernel") if (
+                                       traffic and args.ctx == 131072 and L == 32) else None,
+                                   "launch_us": round(us_sd, 3), "bytes_per_launch": int(sd_bytes)},
         "cpu_baseline": cpu,
         "cells": cells,
         "avg_budget_32": avg32,

@@ -55,7 +55,7 @@
 extern "C" {
 #endif
 
-#define ADAKV_ABI_VERSION 5
+#define ADAKV_ABI_VERSION 6
 
 /* Status codes.  Argument errors are detected on the host before any launch. */
 enum {
@@ -198,6 +198,16 @@ int adakv_decode_fused(const adakv_geometry_t* g, const adakv_query_t* q, const 
                        const adakv_budget_t* budget, const adakv_selection_t* sel,
                        int32_t append_new, float sm_scale, const adakv_output_t* out,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* The first of adakv_decode_fused's two launches, alone and exactly as the step
+ * issues it: the optional summary append of the newest append_new tokens, the
+ * block scores (adakv/estimator.py:62-74) and their per-workgroup softmax
+ * records (the entropy statistics of adakv/budget.py:33-37), left in the
+ * workspace.  For timing the step's launches separately. */
+int adakv_decode_fused_scan(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_kv_t* kv,
+                            const adakv_centroid_t* centroid, const int32_t* seq_lens,
+                            const adakv_budget_t* budget, int32_t append_new, void* workspace,
+                            size_t workspace_bytes, void* stream);
 
 /* adakv_decode_fused without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops or

@@ -134,6 +134,28 @@ def test_noalloc_refuses_a_step_larger_than_its_scratch(lib):
              ctypes.byref(narrow), 1, ctypes.c_float(0.088), ctypes.byref(out), None) == C.ADAKV_ERR_SHAPE
 
 
+def test_scan_launch_validates_on_the_host(lib):
+    """adakv_decode_fused_scan (the step's first launch alone) rejects bad
+    arguments before any launch, as adakv_decode_fused does."""
+    g = _g()
+    q = C.Query(0x1000, C.ADAKV_BF16, 4096, 128)
+    kv = C.KV(0x1000, 0x2000, C.ADAKV_BF16, 8 * 131072 * 128, 131072 * 128, 128)
+    c = C.Centroid(0x4000, C.ADAKV_BF16, C.SUMMARY_CENTROID)
+    bud = _b(avg_budget=8)
+    ws = ctypes.c_void_p(0x10000)
+    f = lib.adakv_decode_fused_scan
+    assert f(ctypes.byref(g), None, ctypes.byref(kv), ctypes.byref(c), None, ctypes.byref(bud), 1, ws, 1 << 30,
+             None) == C.ADAKV_ERR_NULL
+    assert f(ctypes.byref(g), ctypes.byref(q), ctypes.byref(kv), ctypes.byref(c), None, ctypes.byref(bud), -1,
+             ws, 1 << 30, None) == C.ADAKV_ERR_VALUE
+    assert f(ctypes.byref(g), ctypes.byref(q), ctypes.byref(kv), ctypes.byref(c), None, ctypes.byref(bud), 1,
+             ws, 16, None) == C.ADAKV_ERR_WORKSPACE
+    # an append needs the centroid type to pair with K's: fp16 K, bf16 centroids
+    f16kv = C.KV(0x1000, 0x2000, C.ADAKV_F16, 8 * 131072 * 128, 131072 * 128, 128)
+    assert f(ctypes.byref(g), ctypes.byref(q), ctypes.byref(f16kv), ctypes.byref(c), None, ctypes.byref(bud), 1,
+             ws, 1 << 30, None) == C.ADAKV_ERR_DTYPE
+
+
 def test_plan_validation(lib):
     g = _g()
     q = C.Query(0x1000, C.ADAKV_BF16, 4096, 128)

@@ -186,6 +186,31 @@ def test_fused_append_several_rows():
     _run(q, K, V, _params(avg=8), 16, torch.bfloat16, append_new=40, corrupt_tail=40)
 
 
+def test_scan_launch_alone_matches_the_step():
+    """adakv_decode_fused_scan, the step's first launch alone: its append
+    rewrites the stale newest blocks exactly as a rebuild, and the step that
+    follows on the same summaries selects as the whole step does."""
+    say("fused scan launch alone (append 40 tokens)")
+    ops = _ops()
+    q, K, V = _inputs(26, 1, 32, 8, 4096 + 7, 128)
+    qd, kd, vd = (torch.from_numpy(x).to(torch.bfloat16).to(DEV) for x in (q, K, V))
+    kstale = kd.clone()
+    kstale[:, :, K.shape[2] - 40:] = 7.0
+    c = ops.centroid_build(kstale, 16, centroid_dtype=torch.bfloat16)
+    budget = _budget(ops, _params(avg=8))
+    ops.decode_fused_scan(qd, kd, vd, c, 16, budget, append_new=40)
+    fresh = ops.centroid_build(kd, 16, centroid_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(c, fresh), "the scan launch's append differs from a rebuild"
+    _, t1, l1 = ops.decode_fused(qd, kd, vd, c, 16, budget, append_new=40, return_selection=True)
+    _, t2, l2 = ops.decode_fused(qd, kd, vd, fresh, 16, budget, append_new=0, return_selection=True)
+    torch.cuda.synchronize()
+    assert torch.equal(l1, l2)
+    for h in range(l1.shape[1]):
+        n = int(l1[0, h])
+        assert torch.equal(t1[0, h, :n], t2[0, h, :n]), f"head {h}"
+
+
 def test_fused_ragged_batch_with_empty_sequence():
     """Lengths 0, 1, 777 and 4096 in one batch: NaN rows and zero counts for the empty one."""
     say("fused ragged batch [0, 1, 777, 4096]")
