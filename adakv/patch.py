@@ -98,6 +98,41 @@ class _LayerState:
 # Per-layer state keyed by id(module), like the reference's _FROZEN (patch.py:54).
 _STATE: dict[int, _LayerState] = {}
 
+
+def _reorder_states(beam_idx):
+    """Beam search reorders the cache's rows between steps (Cache.reorder_cache,
+    which generate() calls with the surviving beams, repeats allowed).  Each
+    layer's summaries are kept per row, so they follow the same permutation:
+    otherwise the next step would refresh only the newest block of every row
+    and score the rest against another beam's summaries."""
+    for st in _STATE.values():
+        if st.centroid.shape[0] != beam_idx.numel():
+            continue
+        order = beam_idx.tolist()
+        st.centroid = st.centroid.index_select(0, beam_idx.to(st.centroid.device))
+        st.starts = [st.starts[i] for i in order]
+        st.lens = [st.lens[i] for i in order]
+
+
+def _wrap_reorder_cache():
+    try:
+        from transformers.cache_utils import Cache
+    except Exception:  # pragma: no cover - transformers without the Cache class
+        return
+    if getattr(Cache.reorder_cache, "_adakv", False):
+        return
+    base = Cache.reorder_cache
+
+    def reorder_cache(self, beam_idx):
+        base(self, beam_idx)
+        _reorder_states(beam_idx)
+
+    reorder_cache._adakv = True
+    Cache.reorder_cache = reorder_cache
+
+
+_wrap_reorder_cache()
+
 class _Frozen:
     """A layer's retained set, frozen at prefill: mask [Hq, nbp] bool and the
     same blocks as an ascending table [Hq, k] with lens [Hq]."""

@@ -23,6 +23,7 @@ from __future__ import annotations
 import pytest
 
 from gpu_util import DEV, need_gpu, say, torch
+from hook_check import HookCheck
 
 pytestmark = pytest.mark.gpu
 
@@ -170,6 +171,62 @@ def test_normal_budget_realises_the_mean(cache_kind):
     assert len(trace) == STEPS * 2
     assert all(abs(t - 8.0) <= 0.5 for t in trace), trace
     assert torch.isfinite(got).all()
+
+
+@pytest.mark.parametrize("cache_kind", ["dynamic", "static"])
+def test_normal_budget_hook_steps_match_the_oracle(cache_kind):
+    """avg_budget 8 over STEPS steps: at every layer and step the hook's
+    persistent summaries equal a rebuild of the live tokens (the first step
+    builds them, later steps refresh them through append_new, a static cache
+    through its views of the live tokens), the selection equals the oracle's
+    plan on them, and the output equals fp64 attention over it."""
+    from adakv.patch import disable_adakv, enable_adakv
+    say(f"patch bf16 avg_budget 8, {cache_kind} cache: every hook step against the oracle")
+    model = _model(torch.bfloat16)
+    enable_adakv(**_cfg(avg_budget=8))
+    with HookCheck() as hc:
+        _decode_logits(model, _ids(2), cache_kind)
+    disable_adakv()
+    say(f"  {hc.calls} hook calls, {hc.heads - hc.excluded}/{hc.heads} heads compared")
+    assert hc.calls == STEPS * 2 and hc.sequences == STEPS * 2 * 2
+    assert hc.appends == (STEPS - 1) * 2
+
+
+def test_left_padded_normal_budget_hook_steps_match_the_oracle():
+    """A left-padded batch at avg_budget 8: each sequence decodes on its own
+    view (blocks counted from its first real token), and its summaries,
+    selection and output hold at every layer and step."""
+    from adakv.patch import disable_adakv, enable_adakv
+    say("patch left-padded batch of 3, bf16 avg_budget 8: every hook step against the oracle")
+    model = _model(torch.bfloat16)
+    enable_adakv(**_cfg(avg_budget=8))
+    with HookCheck() as hc:
+        _decode_logits(model, _ids(3), "dynamic", attention_mask=_left_padded())
+    disable_adakv()
+    assert hc.calls == STEPS * 2 * 3 and hc.appends == (STEPS - 1) * 2 * 3
+
+
+def test_beam_search_keeps_each_rows_summaries():
+    """generate(num_beams=2) at avg_budget 8: beam search reorders the cache's
+    rows between steps (Cache.reorder_cache); the layers' summaries follow the
+    same permutation, so every step's summaries equal a rebuild of each row's
+    tokens and its selection matches the oracle.  48 new tokens: the beams'
+    own tokens reach blocks that the step's append no longer recomputes, so
+    summaries left unpermuted would show."""
+    from adakv.patch import disable_adakv, enable_adakv
+    say("patch generate(num_beams=2, 48 tokens), bf16 avg_budget 8: summaries follow the beams")
+    model = _model(torch.bfloat16)
+    ids = _ids(1)
+    new = 48
+    enable_adakv(**_cfg(avg_budget=8))
+    with HookCheck() as hc:
+        with torch.no_grad():
+            model.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=new, min_new_tokens=new,
+                           num_beams=2, do_sample=False, pad_token_id=0)
+    disable_adakv()
+    say(f"  {hc.calls} hook calls, {hc.appends} incremental refreshes")
+    assert hc.calls == (new - 1) * 2 and hc.sequences == (new - 1) * 2 * 2
+    assert hc.appends == (new - 2) * 2
 
 
 def test_generate_with_static_cache_matches_sdpa_greedy():

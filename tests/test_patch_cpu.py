@@ -72,3 +72,27 @@ def test_the_adakv_implementation_has_an_sdpa_mask_function():
     from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
     assert ALL_MASK_ATTENTION_FUNCTIONS["adakv"] is sdpa_mask
     assert "adakv" in ALL_ATTENTION_FUNCTIONS
+
+
+def test_beam_reordering_permutes_each_layers_summaries():
+    """Cache.reorder_cache (beam search) also permutes every layer state of the
+    same batch: summaries, starts and lengths follow the beams, repeats
+    included; a state of another batch size is left as it was."""
+    from transformers import DynamicCache
+    st = object.__new__(P._LayerState)
+    st.centroid = torch.arange(3, dtype=torch.float32).view(3, 1, 1, 1).expand(3, 2, 4, 8).clone()
+    st.starts, st.lens = [0, 1, 2], [10, 11, 12]
+    other = object.__new__(P._LayerState)
+    other.centroid = torch.zeros(2, 2, 4, 8)
+    other.starts, other.lens = [0, 0], [5, 5]
+    saved = dict(P._STATE)
+    P._STATE.clear()
+    P._STATE.update({1: st, 2: other})
+    try:
+        DynamicCache().reorder_cache(torch.tensor([2, 0, 0]))
+    finally:
+        P._STATE.clear()
+        P._STATE.update(saved)
+    assert st.centroid[:, 0, 0, 0].tolist() == [2.0, 0.0, 0.0]
+    assert st.starts == [2, 0, 0] and st.lens == [12, 10, 10]
+    assert other.lens == [5, 5] and not other.centroid.any()
