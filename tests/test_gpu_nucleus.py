@@ -96,9 +96,10 @@ def test_nucleus_crossing_in_the_tail_bin(P):
     passes over all 31 bits of the distance.  Centroids are set directly
     (score = q[0] * c[0]).  Counts are held to the oracle's on the GPU's own
     scores wherever NumPy's fp32 running sum fixes them; a tail crossing sums
-    about 10^3 terms of 1e-5, inside that sum's error, so those heads' counts
-    are checked only against the budget bounds (their exact value is not
-    pinned here)."""
+    about 10^3 terms of 1e-5, inside that sum's error, so every head's count
+    is also held to the fp64 cumulative sum of the same fp32 probabilities,
+    which the kernel's exact integer masses reproduce (with at least 4 heads
+    crossing in the tail among those checked)."""
     ops = _ops()
     Hq, Hkv, D, bs, S = 32, 8, 64, 16, 131072
     G = Hq // Hkv
@@ -147,6 +148,33 @@ def test_nucleus_crossing_in_the_tail_bin(P):
     k = lens[0].cpu().numpy()
     floor = min(p["sink"], nb) + min(p["local"], nb) + p["cmin"]
     assert np.all(k >= max(lo, floor)) and np.all(k <= max(min(p["kmax"], nb), floor))
+    # The tail branch pinned against an fp64 cumulative sum.  The weight
+    # kernel adds the probabilities' masses exactly, so its K* is the fp64
+    # count of the same fp32 probabilities wherever the crossing is farther
+    # from P than their own last-ulp differences (2e-7 of the whole mass);
+    # NumPy's fp32 running sum is no reference there (10^3 terms of 1e-5).
+    z = scores.astype(np.float32)
+    p32 = np.exp(z - z.max(axis=1, keepdims=True))
+    p32 /= p32.sum(axis=1, keepdims=True)
+    c64 = np.cumsum(np.sort(p32.astype(np.float64), axis=1)[:, ::-1], axis=1)
+    P32 = float(np.float32(P))
+    w64 = (c64 < P32).sum(axis=1).astype(np.float64) + 1.0
+    edge = np.zeros(Hq, bool)
+    for h in range(Hq):
+        kk = int(w64[h])
+        for j in (kk - 2, kk - 1):
+            if 0 <= j < nb and abs(c64[h, j] - P32) <= 2e-7:
+                edge[h] = True
+    extra64 = O.budget_extra(w64, lo, target)
+    margin64 = max(1e-3, 2.0 * float(edge.sum()) * float(extra64.max()) / float(w64.sum()) + 1e-4)
+    hi = min(p["kmax"], nb)
+    k64 = np.minimum(np.maximum(np.clip(np.round(lo + extra64), lo, hi).astype(np.int64), floor), nb)
+    checked = ~(edge | O.budget_near_half(w64, lo, target, margin=margin64))
+    say(f"  fp64 counts: {int(checked.sum())} heads checked, {int((checked & deep).sum())} crossing in the tail, "
+        f"{int(edge.sum())} at the edge")
+    bad = [(h, int(k[h]), int(k64[h])) for h in range(Hq) if checked[h] and k[h] != k64[h]]
+    assert not bad, f"counts differ from the fp64 nucleus count on heads {bad[:8]}"
+    assert (checked & deep).sum() >= 4, "fewer than 4 tail-crossing heads had their counts checked"
 
 
 def test_nucleus_plan_matches_reference_golden():
