@@ -31,7 +31,7 @@ int ceil_div_h(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 bool valid_dtype(int dt) { return dt == ADAKV_F32 || dt == ADAKV_F16 || dt == ADAKV_BF16; }
 int elt_bytes(int dt) { return dt == ADAKV_F32 ? 4 : 2; }
 int per_vec(int dt) { return 16 / elt_bytes(dt); }
-int gmax_of(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8; }
+int gmax_of(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 16; }
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // Summary element type per key element type: the key type itself or fp32;
@@ -55,7 +55,7 @@ int check_geometry(const adakv_geometry_t* g) {
     return ADAKV_ERR_SHAPE;
   if (g->n_q_heads % g->n_kv_heads) return ADAKV_ERR_SHAPE;
   if ((int64_t)g->max_blocks * g->block_size < g->max_seq_len) return ADAKV_ERR_SHAPE;
-  if (g->n_q_heads / g->n_kv_heads > 8) return ADAKV_ERR_UNSUPPORTED;
+  if (g->n_q_heads / g->n_kv_heads > 16) return ADAKV_ERR_UNSUPPORTED;
   const int D = g->head_dim;
   if (D != 32 && D != 64 && D != 128 && D != 256) return ADAKV_ERR_UNSUPPORTED;
   if (g->max_blocks > kMaxBlocks || g->block_size > 4096) return ADAKV_ERR_UNSUPPORTED;

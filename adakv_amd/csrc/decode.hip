@@ -710,7 +710,8 @@ hipError_t launch_g(const DecodeArgs& a, size_t dyn, hipStream_t s) {
   if (ge <= 1) ADAKV_LAUNCH(1);
   else if (ge <= 2) ADAKV_LAUNCH(2);
   else if (ge <= 4) ADAKV_LAUNCH(4);
-  else ADAKV_LAUNCH(8);
+  else if (ge <= 8) ADAKV_LAUNCH(8);
+  else ADAKV_LAUNCH(16);
 #undef ADAKV_LAUNCH
   return hipGetLastError();
 }

@@ -504,7 +504,8 @@ void launch_score_g(const ScoreArgs& a, dim3 grid, hipStream_t s) {
   if (a.G <= 1) hipLaunchKernelGGL((score_kernel<CDT, D, 1, MM, TPW>), grid, dim3(kNT), 0, s, a);
   else if (a.G <= 2) hipLaunchKernelGGL((score_kernel<CDT, D, 2, MM, TPW>), grid, dim3(kNT), 0, s, a);
   else if (a.G <= 4) hipLaunchKernelGGL((score_kernel<CDT, D, 4, MM, TPW>), grid, dim3(kNT), 0, s, a);
-  else hipLaunchKernelGGL((score_kernel<CDT, D, 8, MM, TPW>), grid, dim3(kNT), 0, s, a);
+  else if (a.G <= 8) hipLaunchKernelGGL((score_kernel<CDT, D, 8, MM, TPW>), grid, dim3(kNT), 0, s, a);
+  else hipLaunchKernelGGL((score_kernel<CDT, D, 16, MM, TPW>), grid, dim3(kNT), 0, s, a);
 }
 
 // Tiles per wave of the matrix-core scan: kScoreTiles, halved while the grid

@@ -71,7 +71,7 @@ def test_table_width_is_the_static_bound(lib):
 
 @pytest.mark.parametrize("bad,code", [
     (dict(Hq=30, Hkv=8), C.ADAKV_ERR_SHAPE),
-    (dict(Hq=72, Hkv=8), C.ADAKV_ERR_UNSUPPORTED),       # group 9 > 8
+    (dict(Hq=136, Hkv=8), C.ADAKV_ERR_UNSUPPORTED),      # group 17 > 16
     (dict(D=96), C.ADAKV_ERR_UNSUPPORTED),
     (dict(max_blocks=100), C.ADAKV_ERR_SHAPE),           # too few blocks for max_seq_len
     (dict(max_seq_len=65536 * 16, max_blocks=65536), C.ADAKV_ERR_UNSUPPORTED),

@@ -2,7 +2,7 @@
 
 * config 2: Llama-3.1-8B layer at context 32768, half the KV heads peaked
   (keys scaled x4), avg_budget 8;
-* config 3: context 131072 with 4 planted needle blocks per KV head (keys of
+* config 3: context 131072 (and 262144) with 4 planted needle blocks per KV head (keys of
   needle j of KV head g = 3 * q[g * G + j] + noise), avg_budget 8 and 32;
 * config 4: ragged batch of 8 sequences, lengths uniform in [16K, 128K], half
   the heads peaked, avg_budget 16.
@@ -134,6 +134,30 @@ def test_needles_two_tiles_per_wave(S):
     table, lens = table[0].cpu().numpy(), lens[0].cpu().numpy()
     q_np = q[0].float().cpu().numpy()
     _oracle_check(q_np, c[0].float().cpu().numpy(), table, lens, avg)
+    assert abs(lens.mean() - avg) <= 1.0
+    _check_output(out[0].float().cpu().numpy(), _ref_selected(q_np, k[0], v[0], table, lens, S))
+
+
+@pytest.mark.parametrize("cdt", [torch.float32, torch.bfloat16])
+def test_needles_256k(cdt):
+    """Context 262,144 (16,384 blocks per KV head): the selection runs at its
+    widest shape (512 threads, 32 blocks per thread), the matrix-core scan
+    (bf16 centroids) at 4 tiles per wave; every q-head finds its own needle."""
+    ops = _ops()
+    S, avg = 262144, 8
+    say(f"needles: ctx {S}, avg_budget {avg}, centroids {cdt}")
+    q, k, v, pos = _needle_layer(S, seed=13)
+    c = ops.centroid_build(k, BS, centroid_dtype=cdt)
+    out, table, lens = ops.decode_fused(q, k, v, c, BS, ops.BudgetParams(avg_budget=avg),
+                                        append_new=1, return_selection=True)
+    torch.cuda.synchronize()
+    table, lens = table[0].cpu().numpy(), lens[0].cpu().numpy()
+    q_np = q[0].float().cpu().numpy()
+    _oracle_check(q_np, c[0].float().cpu().numpy(), table, lens, avg)
+    for g in range(HKV):
+        for j in range(4):
+            h = g * G + j
+            assert int(pos[g, j]) in set(table[h, : lens[h]].tolist()), f"head {h} missed its needle"
     assert abs(lens.mean() - avg) <= 1.0
     _check_output(out[0].float().cpu().numpy(), _ref_selected(q_np, k[0], v[0], table, lens, S))
 

@@ -163,12 +163,40 @@ def _inputs(seed, B, Hq, Hkv, S, D, peaked=True):
     return q, K, V
 
 
-@pytest.mark.parametrize("Hq,Hkv,D", [(64, 8, 64), (48, 8, 32), (40, 5, 128)])
+@pytest.mark.parametrize("Hq,Hkv,D", [(64, 8, 64), (48, 8, 32), (40, 5, 128), (128, 8, 128), (32, 2, 64)])
 def test_fused_many_heads(Hq, Hkv, D):
-    """More q-heads than one merge pass covers (32 per pass)."""
+    """More q-heads than one merge pass covers (32 per pass); groups of 16
+    q-heads per KV head (128 q / 8 KV heads, the largest group accepted)."""
     say(f"fused Hq={Hq} Hkv={Hkv} D={D}")
     q, K, V = _inputs(21, 1, Hq, Hkv, 4096, D)
     _run(q, K, V, _params(avg=10), 16, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+def test_fused_group16_other_dtypes(dt):
+    """Group 16 with fp32 K/V (the exact mode: its vector-unit scan and decode)
+    and fp16, a ragged batch of two."""
+    say(f"fused 128 q / 8 KV heads, {dt}")
+    q, K, V = _inputs(23, 2, 128, 8, 3000, 64)
+    _run(q, K, V, _params(avg=12), 16, dt, seq_lens=[3000, 1777])
+
+
+def test_group16_plan_then_sparse_decode():
+    """128 q / 8 KV heads through plan + table-driven decode: the plan's
+    selection against the oracle and the decode against fp64 attention over it."""
+    ops = _ops()
+    say("plan + sparse decode, 128 q / 8 KV heads")
+    q, K, V = _inputs(27, 1, 128, 8, 6000, 128)
+    dt = torch.bfloat16
+    qd, kd, vd = (torch.from_numpy(x).to(dt).to(DEV) for x in (q, K, V))
+    c = ops.centroid_build(kd, 16, centroid_dtype=dt)
+    budget = ops.BudgetParams(avg_budget=8)
+    table, lens = ops.plan(qd, c, 16, budget, seq_len=6000)
+    out = ops.sparse_decode(qd, kd, vd, table, lens, 16)
+    torch.cuda.synchronize()
+    _check_sequence(_rounded(q[0], dt), _rounded(K[0], dt), _rounded(V[0], dt), c[0].float().cpu().numpy(),
+                    table[0].cpu().numpy(), lens[0].cpu().numpy(), out[0].float().cpu().numpy(),
+                    _params(avg=8), 16, "plan + sparse decode")
 
 
 @pytest.mark.parametrize("bs", [24, 32, 8])

@@ -232,6 +232,9 @@ def _random_table(rng, Hq, nb, width, lens):
     (2, 3, 777, 32, 8, torch.bfloat16),         # blocks shorter than a 16-token tile
     (2, 4, 1500, 64, 24, torch.float16),        # blocks of 1.5 tiles, padded q-heads
     (2, 2, 600, 256, 16, torch.bfloat16),
+    (8, 16, 2048, 128, 16, torch.bfloat16),     # GQA 16: 128 q / 8 KV heads
+    (1, 16, 700, 256, 16, torch.float32),       # GQA 16, head_dim 256, vector-unit decode
+    (2, 16, 900, 64, 24, torch.float16),
 ])
 def test_sparse_decode_matches_same_selection_reference(Hkv, group, S, D, bs, dt):
     ops = _ops()
@@ -318,11 +321,12 @@ def test_fused_step_matches_oracle_output(name):
     assert np.abs(got - ref).max() <= 2e-4
 
 
-@pytest.mark.parametrize("S,dt", [(4096, torch.float32), (20000, torch.bfloat16), (777, torch.float16)])
-def test_dense_decode_matches_fp64_dense(S, dt):
+@pytest.mark.parametrize("S,dt,G", [(4096, torch.float32, 4), (20000, torch.bfloat16, 4), (777, torch.float16, 4),
+                                    (5000, torch.bfloat16, 16), (1000, torch.float32, 16)])
+def test_dense_decode_matches_fp64_dense(S, dt, G):
     ops = _ops()
-    say(f"dense decode S={S} {dt}")
-    Hkv, G, D = 8, 4, 128
+    say(f"dense decode S={S} {dt} group {G}")
+    Hkv, D = 8, 128
     q = torch.randn(1, Hkv * G, D).to(dt)
     k = torch.randn(1, Hkv, S, D).to(dt)
     v = torch.randn(1, Hkv, S, D).to(dt)
