@@ -62,6 +62,7 @@ struct StepLds {
   float tau;
   alignas(16) uint64_t keys[kSortCap];                        // general selection: selected keys
   int list[kSortCap];                                         // content blocks by rank (general path)
+  alignas(16) uint16_t q[D];                                  // the query (16-bit, K's type)
   uint32_t vt[(NT / kWave) * TileShape<D>::VT_WORDS];         // the waves' V tiles
   float m[NT / kWave], l[NT / kWave];
   float acc[NT / kWave][D];
@@ -342,9 +343,15 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   const int hl = tid & (LPH - 1);
   const float* parts_b = a.parts + (int64_t)b * Hq * a.parts_pitch * kPartFloats;
   const float* scores_b = a.scores + (int64_t)b * Hq * a.sp;
+  // (records group-major: a wave's loads of one group of consecutive records
+  // are contiguous.  Every load of this phase is unconditional, its index
+  // clamped in bounds: the compiler counts outstanding loads per path and, where
+  // paths join, waits as if the fewest had been issued, so one load under a
+  // branch before the tile loads makes the first use of the records wait for
+  // the tiles too)
   auto rec4 = [&](int hh, int j, int g) {    // 16-byte group g of record j of head hh
-    return *reinterpret_cast<const float4*>(parts_b + (hh * a.parts_pitch + min(j, max(n_ck - 1, 0))) * kPartFloats +
-                                            4 * g);
+    return *reinterpret_cast<const float4*>(parts_b + ((int64_t)(hh * kPartGroups + g) * a.parts_pitch +
+                                                       min(j, max(n_ck - 1, 0))) * 4);
   };
   auto extra = [&](int hh, int e) { return scores_b[hh * a.sp + min(rows_in_chunks + e, nb - 1)]; };
   const int hh0 = tid / LPH;
@@ -363,22 +370,18 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   const float4 C1 = rec4(h, lane, 1), C2 = rec4(h, lane, 2), C3 = rec4(h, lane, 3), C4 = rec4(h, lane, 4);
   const float XE = extra(h, lane);
   __builtin_amdgcn_sched_barrier(0);
-  // (c) the query (same 16-bit type as K, 16-byte aligned rows), as the B
-  //     operand of S^T: lane (col, grp) holds q[D/4*grp + 8*s .. +7] in every
-  //     column (columns other than 0 are masked out of the softmax)
-  uint4 qf[D / 32];
-  {
-    const uint16_t* qp = reinterpret_cast<const uint16_t*>(d.q) + (int64_t)b * d.qsb + (int64_t)h * d.qsh + (D / 4) * grp;
-#pragma unroll
-    for (int s2 = 0; s2 < D / 32; ++s2) qf[s2] = *reinterpret_cast<const uint4*>(qp + 8 * s2);
-  }
+  // (c) the query (same 16-bit type as K, 16-byte aligned rows): 16 bytes per
+  //     thread of the first D / 8, stored to LDS at the end of phase 1 (a store
+  //     now would wait for this wave's loads before its tile loads issue)
+  const uint4 qv = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(d.q) + (int64_t)b * d.qsb +
+                                                   (int64_t)h * d.qsh + 8 * (tid & (D / 8 - 1)));
   __builtin_amdgcn_sched_barrier(0);
   // (d) the decode's items: item j is 16-token sub-tile j % n_sub of list
   //     entry j / n_sub; entries [0, nf) are the sink then the local blocks
   //     (the table row's order), later ones the content blocks by rank.  The
-  //     first two items of this wave, when forced, are loaded now (only the
-  //     waves that own such an item load it: a CU takes in 64 bytes per
-  //     clock, so a load for nothing delays the useful loads of its other waves)
+  //     first PF items of this wave, when forced, are loaded now; a wave with
+  //     fewer forced items re-reads the last forced one (cache hits), so that
+  //     the load count is the same on every path)
   const int n_sub = (a.bs + 15) >> 4;
   const int nf_items = nf * n_sub;
   const int64_t head_off = ((int64_t)b * d.sb + (int64_t)(h / d.G) * d.sh + (D / 4) * grp) * 2;
@@ -396,63 +399,25 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   constexpr int PF = NT == 256 ? 2 : 1;
   TileBuf<D> P0, P1;
   int p00 = 0, p01 = 1, p10 = 0, p11 = 1;
+  auto forced_item = [&](int j, int& t0, int& t_hi) {      // j clamped to the forced items
+    j = min(j, max(nf_items - 1, 0));
+    tokens(min(forced_block(j / n_sub), nb - 1), j % n_sub, t0, t_hi);
+  };
   if constexpr (PF >= 1) {
-    if (wu < nf_items) {
-      tokens(forced_block(wu / n_sub), wu % n_sub, p00, p01);
-      tile_load<D>(kbase, vbase, row_bytes, p00, p01, P0);
-    }
+    forced_item(wu, p00, p01);
+    tile_load<D>(kbase, vbase, row_bytes, p00, p01, P0);
   }
   if constexpr (PF >= 2) {
-    if (wu + NW < nf_items) {
-      tokens(forced_block((wu + NW) / n_sub), (wu + NW) % n_sub, p10, p11);
-      tile_load<D>(kbase, vbase, row_bytes, p10, p11, P1);
-    }
+    forced_item(wu + NW, p10, p11);
+    tile_load<D>(kbase, vbase, row_bytes, p10, p11, P1);
   }
   __builtin_amdgcn_sched_barrier(0);
   const double lognb = log((double)max(nb, 2));   // while the loads are in flight
 
-  // ---- 1. weights of every head; the pool's first ranks ----
-  const float tf = (float)fmax(a.cfg.temperature, 1e-6);
-  auto merge_head = [&](int hh, const float4 (&Q)[kRecsUpFront], float X) {
-    const bool on = hh < Hq;
-    SoftPart pt = soft_empty();
-    if (on) {
-#pragma unroll
-      for (int u = 0; u < kRecsUpFront; ++u)
-        if (hl + LPH * u < n_ck) pt = soft_merge(pt, SoftPart{Q[u].x, Q[u].y, Q[u].z});
-      for (int j = hl + LPH * kRecsUpFront; j < n_ck; j += LPH) {   // long contexts
-        const float4 q4 = rec4(hh, j, 0);
-        pt = soft_merge(pt, SoftPart{q4.x, q4.y, q4.z});
-      }
-      if (hl < n_extra) pt = soft_merge(pt, SoftPart{tf == 1.f ? X : __fdiv_rn(X, tf), 1.f, 0.f});
-      for (int e = hl + LPH; e < n_extra; e += LPH) {
-        const float x = extra(hh, e);
-        pt = soft_merge(pt, SoftPart{tf == 1.f ? x : __fdiv_rn(x, tf), 1.f, 0.f});
-      }
-    }
-    switch (LPH) {                          // uniform
-      case 16: pt = soft_group_merge<16>(pt); break;
-      case 8: pt = soft_group_merge<8>(pt); break;
-      case 4: pt = soft_group_merge<4>(pt); break;
-      case 2: pt = soft_group_merge<2>(pt); break;
-      default: break;
-    }
-    if (on && hl == 0) s_w[hh] = entropy_weight(pt, lognb);
-  };
-  if (adaptive) {
-    merge_head(hh0, R, X0);
-    for (int p = 1; p * (NT / LPH) < Hq; ++p) {    // more heads than NT / LPH
-      const int hh = p * (NT / LPH) + tid / LPH;
-      const int hs = min(hh, Hq - 1);
-      float4 Q[kRecsUpFront];
-#pragma unroll
-      for (int u = 0; u < kRecsUpFront; ++u) Q[u] = rec4(hs, hl + LPH * u, 0);
-      merge_head(hh, Q, extra(hs, hl));
-    }
-  } else if (nucleus) {
-    if (tid < Hq) s_w[tid] = W0;
-    for (int hh = tid + NT; hh < Hq; hh += NT) s_w[hh] = a.wbuf[(int64_t)b * Hq + hh];
-  }
+  // ---- 1. the pool's first ranks (first: no branch between the loads and
+  //      this use of the pool records, so the wait for them is exact and the
+  //      content tile prefetch below issues as early as it can), then the
+  //      weights of every head ----
   // The pool: entries (score, block) of this lane; every content block outside
   // it scores at most the largest bound of its sub-chunk.
   float pv[kPool];
@@ -530,6 +495,48 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
       tile_load<D>(kbase, vbase, row_bytes, ca0, ca1, CA);
     }
   }
+  const float tf = (float)fmax(a.cfg.temperature, 1e-6);
+  auto merge_head = [&](int hh, const float4 (&Q)[kRecsUpFront], float X) {
+    const bool on = hh < Hq;
+    SoftPart pt = soft_empty();
+    if (on) {
+#pragma unroll
+      for (int u = 0; u < kRecsUpFront; ++u)
+        if (hl + LPH * u < n_ck) pt = soft_merge(pt, SoftPart{Q[u].x, Q[u].y, Q[u].z});
+      for (int j = hl + LPH * kRecsUpFront; j < n_ck; j += LPH) {   // long contexts
+        const float4 q4 = rec4(hh, j, 0);
+        pt = soft_merge(pt, SoftPart{q4.x, q4.y, q4.z});
+      }
+      if (hl < n_extra) pt = soft_merge(pt, SoftPart{tf == 1.f ? X : __fdiv_rn(X, tf), 1.f, 0.f});
+      for (int e = hl + LPH; e < n_extra; e += LPH) {
+        const float x = extra(hh, e);
+        pt = soft_merge(pt, SoftPart{tf == 1.f ? x : __fdiv_rn(x, tf), 1.f, 0.f});
+      }
+    }
+    switch (LPH) {                          // uniform
+      case 16: pt = soft_group_merge<16>(pt); break;
+      case 8: pt = soft_group_merge<8>(pt); break;
+      case 4: pt = soft_group_merge<4>(pt); break;
+      case 2: pt = soft_group_merge<2>(pt); break;
+      default: break;
+    }
+    if (on && hl == 0) s_w[hh] = entropy_weight(pt, lognb);
+  };
+  if (adaptive) {
+    merge_head(hh0, R, X0);
+    for (int p = 1; p * (NT / LPH) < Hq; ++p) {    // more heads than NT / LPH
+      const int hh = p * (NT / LPH) + tid / LPH;
+      const int hs = min(hh, Hq - 1);
+      float4 Q[kRecsUpFront];
+#pragma unroll
+      for (int u = 0; u < kRecsUpFront; ++u) Q[u] = rec4(hs, hl + LPH * u, 0);
+      merge_head(hh, Q, extra(hs, hl));
+    }
+  } else if (nucleus) {
+    if (tid < Hq) s_w[tid] = W0;
+    for (int hh = tid + NT; hh < Hq; hh += NT) s_w[hh] = a.wbuf[(int64_t)b * Hq + hh];
+  }
+  if (tid < D / 8) *reinterpret_cast<uint4*>(&L.q[8 * tid]) = qv;
   lds_barrier();
 
   // ---- 2. the head's count (every wave) ----
@@ -688,6 +695,12 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   }
 
   // ---- 4. flash-decode over the k blocks ----
+  // the query as the B operand of S^T: lane (col, grp) holds
+  // q[D/4*grp + 8*s .. +7] in every column (columns other than 0 are masked
+  // out of the softmax)
+  uint4 qf[D / 32];
+#pragma unroll
+  for (int s2 = 0; s2 < D / 32; ++s2) qf[s2] = *reinterpret_cast<const uint4*>(&L.q[(D / 4) * grp + 8 * s2]);
   TileState<D> st;
   tile_init(st);
   {

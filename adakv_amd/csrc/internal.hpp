@@ -38,7 +38,7 @@ struct ScoreArgs {
   int kdt;
   int64_t ksb, ksh, kss;
   // softmax records of the scores (nullptr: not wanted), one per (sequence,
-  // q-head, score workgroup) at parts[((b * Hq + h) * parts_pitch + unit) * kPartFloats]
+  // q-head, score workgroup): group g of record `unit` at part_offset(...)
   float* parts;
   int parts_pitch;
   BudgetCfg cfg;
@@ -53,6 +53,14 @@ struct ScoreArgs {
 // exp(z - m), T = sum exp(z - m) * (z - m)) and the exact top two content
 // blocks of each of its 4 sub-chunks and a bound of the rest.  20 floats (80 bytes).
 constexpr int kPartFloats = 20;
+constexpr int kPartGroups = kPartFloats / 4;
+// Records are stored group-major per (sequence, q-head): the 16-byte group g
+// of records 0, 1, 2, ... lies in consecutive words, so a wave whose lane l
+// reads group g of record l reads one contiguous KiB (an 80-byte record
+// stride would touch a cache line per lane).  Offset in floats.
+__host__ __device__ __forceinline__ int64_t part_offset(int b, int Hq, int h, int pitch, int slot, int g) {
+  return ((((int64_t)b * Hq + h) * kPartGroups + g) * pitch + slot) * 4;
+}
 
 struct SelectArgs {
   const float* scores;

@@ -72,9 +72,8 @@ __global__ __launch_bounds__(NT) void select_kernel(SelectArgs a) {
   SoftPart pt = soft_empty();
   bool has = false;
   for (int c = tid; c < n_ck; c += NT) {
-    const float4* rec = reinterpret_cast<const float4*>(a.parts + (((int64_t)b * a.Hq + h) * a.parts_pitch + c) *
-                                                                  kPartFloats);
-    const float4 r0 = rec[0], r1 = rec[1];
+    const float4 r0 = *reinterpret_cast<const float4*>(a.parts + part_offset(b, a.Hq, h, a.parts_pitch, c, 0));
+    const float4 r1 = *reinterpret_cast<const float4*>(a.parts + part_offset(b, a.Hq, h, a.parts_pitch, c, 1));
     pt = soft_merge(pt, SoftPart{r0.x, r0.y, r0.z});
     const float mx[4] = {r1.x, r1.y, r1.z, r1.w};   // the sub-chunks' largest content scores
 #pragma unroll

@@ -124,13 +124,13 @@ __device__ __forceinline__ void append_block(const ScoreArgs& a, int b, int kvh,
 // sub-chunks with a bound of the rest (layout in select.hpp).
 __device__ __forceinline__ void write_part(const ScoreArgs& a, int b, int h, int slot, float m, float S, float T,
                                            const Top2 (&t)[4]) {
-  float4* rec = reinterpret_cast<float4*>(a.parts + (((int64_t)b * a.Hq + h) * a.parts_pitch + slot) * kPartFloats);
+  auto rec = [&](int g) { return reinterpret_cast<float4*>(a.parts + part_offset(b, a.Hq, h, a.parts_pitch, slot, g)); };
   auto pk = [](const Top2& x) { return __uint_as_float(((uint32_t)x.r1 & 0xffffu) | ((uint32_t)x.r2 << 16)); };
-  rec[0] = make_float4(m, S, T, 0.f);
-  rec[1] = make_float4(t[0].v1, t[1].v1, t[2].v1, t[3].v1);
-  rec[2] = make_float4(t[0].v2, t[1].v2, t[2].v2, t[3].v2);
-  rec[3] = make_float4(t[0].v3, t[1].v3, t[2].v3, t[3].v3);
-  rec[4] = make_float4(pk(t[0]), pk(t[1]), pk(t[2]), pk(t[3]));
+  *rec(0) = make_float4(m, S, T, 0.f);
+  *rec(1) = make_float4(t[0].v1, t[1].v1, t[2].v1, t[3].v1);
+  *rec(2) = make_float4(t[0].v2, t[1].v2, t[2].v2, t[3].v2);
+  *rec(3) = make_float4(t[0].v3, t[1].v3, t[2].v3, t[3].v3);
+  *rec(4) = make_float4(pk(t[0]), pk(t[1]), pk(t[2]), pk(t[3]));
 }
 
 // fp32 centroids: one workgroup per chunk of CB blocks; every centroid row is

@@ -76,7 +76,8 @@ __device__ __forceinline__ int popcnt(M m) {
 // sum p log p = T / S - log S over the whole set.
 //
 // Record written by the score kernel per (sequence, q-head, score workgroup),
-// kPartFloats = 20 floats in five 16-byte groups:
+// kPartFloats = 20 floats in five 16-byte groups (stored group-major, at
+// part_offset()):
 //   [0..3]   m, S, T of the workgroup's rows, one unused float;
 //   [4..7]   the largest sanitised content score of each of its 4 sub-chunks
 //            (the rows of one wave; -inf: no content block);
