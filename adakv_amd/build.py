@@ -31,6 +31,18 @@ FLAGS = [
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 
+# Per-source additions.  The fused step keeps its matrix-core accumulators in
+# ordinary VGPRs: with the default heuristic they live in AGPRs, and the
+# online-softmax rescale between tiles then copies all of them out and back.
+EXTRA_FLAGS = {
+    "fused.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
+def flags_for(src: str) -> list:
+    return [*FLAGS, *EXTRA_FLAGS.get(src, [])]
+
 
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
@@ -51,7 +63,7 @@ def build(verbose: bool = False) -> str:
 
     def compile_one(src: str) -> str:
         obj = os.path.join(BUILD_DIR, src.replace(".hip", ".o"))
-        cmd = [cc, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+        cmd = [cc, *flags_for(src), "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         r = subprocess.run(cmd, capture_output=True, text=True)

@@ -42,10 +42,18 @@ __device__ __forceinline__ float4_t mfma_pv(const uint2& p, const uint2& v, floa
     return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, p),
                                                  __builtin_bit_cast(f16x4_t, v), c, 0, 0, 0);
 }
+// Two floats to the 16-bit type, round to nearest even (one packed convert
+// instruction on gfx950: v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32).
 template <int KVDT>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  if constexpr (KVDT == ADAKV_BF16) return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
-  else return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  if constexpr (KVDT == ADAKV_BF16) {
+    typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2_t{lo, hi}), b2_t));
+  } else {
+    typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2_t{lo, hi}), h2_t));
+  }
 }
 
 template <int D>
