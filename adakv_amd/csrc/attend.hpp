@@ -130,10 +130,12 @@ __device__ __forceinline__ void tile_load(const char* kbase, const char* vbase, 
 
 // One tile into the state.  head_on: head col takes part in this tile (lanes
 // whose head is off give it zero weight).  vt: this wave's V tile in LDS.
-// scale: sm_scale * log2(e).
+// scale: sm_scale * log2(e).  rescale (uniform): false for the wave's first
+// tile, whose accumulators are still zero and need no rescaling.
 template <int KVDT, int D>
 __device__ __forceinline__ void tile_update(TileState<D>& st, const TileBuf<D>& r, const uint4 (&qf)[D / 32],
-                                            uint32_t* vt, int t0, int t_hi, bool head_on, float scale) {
+                                            uint32_t* vt, int t0, int t_hi, bool head_on, float scale,
+                                            bool rescale = true) {
   using S = TileShape<D>;
   constexpr int KS = S::KS, NT16 = S::NT16, VROW = S::VROW;
   const int lane = threadIdx.x & (kWave - 1), col = lane & 15, grp = lane >> 4;
@@ -176,14 +178,16 @@ __device__ __forceinline__ void tile_update(TileState<D>& st, const TileBuf<D>& 
   st.l_h = st.l_h * alpha + ps;
   st.m_h = mn;
   // rescale the O rows (heads 4*grp+i) by their heads' alpha, held by lanes col == head
-  float al[4];
+  if (rescale) {
+    float al[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    al[i] = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * grp + i) * 4, __float_as_int(alpha)));
+    for (int i = 0; i < 4; ++i)
+      al[i] = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * grp + i) * 4, __float_as_int(alpha)));
 #pragma unroll
-  for (int n = 0; n < NT16; ++n)
+    for (int n = 0; n < NT16; ++n)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st.acc[n][i] *= al[i];
+      for (int i = 0; i < 4; ++i) st.acc[n][i] *= al[i];
+  }
   // O += P . V: A = P[head col][tokens 4*grp .. +3] (the S^T layout), B = V[tokens][16 dims]
   const uint2 pf = make_uint2(pack2<KVDT>(sv[0], sv[1]), pack2<KVDT>(sv[2], sv[3]));
 #pragma unroll

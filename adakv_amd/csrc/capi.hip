@@ -225,6 +225,12 @@ int run_scores(const adakv_geometry_t* g, const adakv_query_t* q, const adakv_ce
   se.chunk_shift = __builtin_ctz((unsigned)sa.chunk_rows);
   se.bs_shift = (g->block_size & (g->block_size - 1)) == 0 ? __builtin_ctz((unsigned)g->block_size) : -1;
   se.n_new = n_new;
+  // the entropy weight's divisor np.log(nb) (adakv/budget.py:35), by the host's
+  // libm as NumPy computes it, for the one length every sequence has
+  if (lens == nullptr) {
+    const int nbu = (g->max_seq_len + g->block_size - 1) / g->block_size;
+    se.lognb_uniform = std::log((double)std::max(nbu, 2));
+  }
   return ADAKV_OK;
 }
 

@@ -80,6 +80,12 @@ __device__ __forceinline__ int lanes_per_head(int Hq) {
 // x / d, with s = log2(d) when d is a power of two (else -1).
 __device__ __forceinline__ int div_p2(int x, int d, int s) { return s >= 0 ? (x >> s) : x / d; }
 
+// x / d and x % d for x >= 0 and a uniform d > 0: a shift or mask when d is a
+// power of two (the usual case: q-heads, GQA group, lanes per head, 16-token
+// tiles per block), the expanded integer division otherwise.
+__device__ __forceinline__ int div_u(int x, int d) { return (d & (d - 1)) == 0 ? (x >> __builtin_ctz(d)) : x / d; }
+__device__ __forceinline__ int mod_u(int x, int d) { return (d & (d - 1)) == 0 ? (x & (d - 1)) : x % d; }
+
 __device__ __forceinline__ double readlane_d(double x, int l) {
   const long long u = __double_as_longlong(x);
   const int lo = __builtin_amdgcn_readlane((int)(u & 0xffffffffll), l);
@@ -308,8 +314,8 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
     // (uniform values kept in scalar registers: a length loaded from memory
     // or a division expanded on the vector unit would otherwise drag every
     // bound and address derived from it onto the vector unit)
-    h = __builtin_amdgcn_readfirstlane(pos % gridDim.x);
-    b = __builtin_amdgcn_readfirstlane(pos / gridDim.x);
+    h = __builtin_amdgcn_readfirstlane(mod_u(pos, gridDim.x));
+    b = __builtin_amdgcn_readfirstlane(div_u(pos, gridDim.x));
   }
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -354,7 +360,7 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
                                                        min(j, max(n_ck - 1, 0))) * 4);
   };
   auto extra = [&](int hh, int e) { return scores_b[hh * a.sp + min(rows_in_chunks + e, nb - 1)]; };
-  const int hh0 = tid / LPH;
+  const int hh0 = div_u(tid, LPH);
   const int hs0 = min(hh0, Hq - 1);
   float4 R[kRecsUpFront];
 #pragma unroll
@@ -384,7 +390,7 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   //     the load count is the same on every path)
   const int n_sub = (a.bs + 15) >> 4;
   const int nf_items = nf * n_sub;
-  const int64_t head_off = ((int64_t)b * d.sb + (int64_t)(h / d.G) * d.sh + (D / 4) * grp) * 2;
+  const int64_t head_off = ((int64_t)b * d.sb + (int64_t)div_u(h, d.G) * d.sh + (D / 4) * grp) * 2;
   const char* kbase = reinterpret_cast<const char*>(d.k) + head_off;
   const char* vbase = reinterpret_cast<const char*>(d.v) + head_off;
   const int64_t row_bytes = d.ss * 2;
@@ -401,7 +407,7 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   int p00 = 0, p01 = 1, p10 = 0, p11 = 1;
   auto forced_item = [&](int j, int& t0, int& t_hi) {      // j clamped to the forced items
     j = min(j, max(nf_items - 1, 0));
-    tokens(min(forced_block(j / n_sub), nb - 1), j % n_sub, t0, t_hi);
+    tokens(min(forced_block(div_u(j, n_sub)), nb - 1), mod_u(j, n_sub), t0, t_hi);
   };
   if constexpr (PF >= 1) {
     forced_item(wu, p00, p01);
@@ -412,7 +418,7 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
     tile_load<D>(kbase, vbase, row_bytes, p10, p11, P1);
   }
   __builtin_amdgcn_sched_barrier(0);
-  const double lognb = log((double)max(nb, 2));   // while the loads are in flight
+  const double lognb = a.seq_lens == nullptr ? a.lognb_uniform : log((double)max(nb, 2));
 
   // ---- 1. the pool's first ranks (first: no branch between the loads and
   //      this use of the pool records, so the wait for them is exact and the
@@ -524,8 +530,8 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   };
   if (adaptive) {
     merge_head(hh0, R, X0);
-    for (int p = 1; p * (NT / LPH) < Hq; ++p) {    // more heads than NT / LPH
-      const int hh = p * (NT / LPH) + tid / LPH;
+    for (int p = 1; p * div_u(NT, LPH) < Hq; ++p) {    // more heads than NT / LPH
+      const int hh = p * div_u(NT, LPH) + div_u(tid, LPH);
       const int hs = min(hh, Hq - 1);
       float4 Q[kRecsUpFront];
 #pragma unroll
@@ -706,8 +712,10 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   {
     uint32_t* vt = L.vt + wu * TileShape<D>::VT_WORDS;
     const float scale = d.scale_log2;
+    bool started = false;                    // uniform: a tile is in the accumulators
     auto compute = [&](int t0, int t_hi, const TileBuf<D>& r) {
-      tile_update<KVDT, D>(st, r, qf, vt, t0, t_hi, col == 0, scale);
+      tile_update<KVDT, D>(st, r, qf, vt, t0, t_hi, col == 0, scale, started);
+      started = true;
     };
     auto load_compute = [&](int blk, int sub) {
       TileBuf<D> X;
@@ -728,7 +736,7 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
     if constexpr (PF >= 2) {
       if (f1) compute(p10, p11, P1);
     }
-    for (int j = wu + PF * NW; j < min(nf_items, n_items); j += NW) load_compute(forced_block(j / n_sub), j % n_sub);
+    for (int j = wu + PF * NW; j < min(nf_items, n_items); j += NW) load_compute(forced_block(div_u(j, n_sub)), mod_u(j, n_sub));
     // (b) the content blocks: item i (sub-tile i % n_sub of the block of rank
     // i / n_sub) on wave (nf_items + i) % NW, so this wave's are rho, rho + NW,
     // ...; the block of a rank is a ballot away in the pool and fast paths
@@ -750,13 +758,13 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
     // item n's compute; the first item may be the tile prefetched before the
     // count
     auto fetch = [&](int it, TileBuf<D>& T, int& t0, int& t1) {
-      const int blk = block_of(it / n_sub);
+      const int blk = block_of(div_u(it, n_sub));
       if (it == rho && n_sub == 1 && blk == cablk) {
         T = CA;
         t0 = ca0;
         t1 = ca1;
       } else {
-        tokens(blk, it % n_sub, t0, t1);
+        tokens(blk, mod_u(it, n_sub), t0, t1);
         tile_load<D>(kbase, vbase, row_bytes, t0, t1, T);
       }
     };

@@ -77,6 +77,7 @@ struct SelectArgs {
   int chunk_shift;             // log2(chunk_rows) (a power of two)
   int bs_shift;                // log2(bs) when bs is a power of two, else -1
   int n_new;                   // rows >= first appended block are not in any chunk partial
+  double lognb_uniform;        // log(max(nb, 2)) of uniform_len, computed on the host (seq_lens null)
 };
 
 struct BudgetArgs {
