@@ -49,7 +49,9 @@ namespace {
 constexpr int kFastKC = 16;         // KC up to this: tau by repeated wave maxima
 constexpr int kRadixKC = 64;        // KC up to this: tau by two radix passes (else the general selection)
 constexpr int kCandLanes = 2;       // candidates per lane on the fast path
-constexpr int kRecsUpFront = 4;     // records per lane loaded in phase 0
+constexpr int kRecsUpFront = 8;     // records per lane loaded in phase 0
+constexpr int kPoolWave = 3;        // the wave that ranks the candidate pool in phase 1
+constexpr int kWeightLanes = kPoolWave * 64;   // waves 0..2 compute the heads' weights
 
 template <int NT, int D>
 struct StepLds {
@@ -60,6 +62,10 @@ struct StepLds {
   int rd[4];                                                  // radix digit and count above
   int sc[NT / kWave];                                         // scan scratch
   float tau;
+  alignas(16) uint64_t pool_pk[kWave];                        // the pool wave's ranked candidates
+  int pool_rank[kWave];                                       //   and their ranks
+  int pool_n;                                                 //   count (-1: more than a wave)
+  float pool_bound;                                           //   bound of every entry outside it
   alignas(16) uint64_t keys[kSortCap];                        // general selection: selected keys
   int list[kSortCap];                                         // content blocks by rank (general path)
   alignas(16) uint16_t q[D];                                  // the query (16-bit, K's type)
@@ -69,7 +75,7 @@ struct StepLds {
 };
 
 // Lanes merging one head's records: the largest power of two with
-// Hq * LPH <= NT, at most 16 (4 for Hq = 64, 8 for Hq = 32 with 256 threads).
+// Hq * LPH <= NT, at most 16 (2 for Hq = 64, 4 for Hq = 32 over 192 lanes).
 template <int NT>
 __device__ __forceinline__ int lanes_per_head(int Hq) {
   int l = 16;
@@ -345,7 +351,7 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   const int rows_in_chunks = min(nb, first_app);
   const int n_ck = (rows_in_chunks + a.chunk_rows - 1) >> a.chunk_shift;   // records per head
   const int n_extra = nb - rows_in_chunks;                                 // rows no record covers
-  const int LPH = lanes_per_head<NT>(Hq);
+  const int LPH = lanes_per_head<kWeightLanes>(Hq);
   const int hl = tid & (LPH - 1);
   const float* parts_b = a.parts + (int64_t)b * Hq * a.parts_pitch * kPartFloats;
   const float* scores_b = a.scores + (int64_t)b * Hq * a.sp;
@@ -420,16 +426,16 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   __builtin_amdgcn_sched_barrier(0);
   const double lognb = a.seq_lens == nullptr ? a.lognb_uniform : log((double)max(nb, 2));
 
-  // ---- 1. the pool's first ranks (first: no branch between the loads and
-  //      this use of the pool records, so the wait for them is exact and the
-  //      content tile prefetch below issues as early as it can), then the
-  //      weights of every head ----
+  // ---- 1. the candidate pool's first NW ranks on the pool wave, the weights of
+  //      every head on waves 0..2 (two independent chains on separate SIMDs) ----
   // The pool: entries (score, block) of this lane; every content block outside
-  // it scores at most the largest bound of its sub-chunk.
+  // it scores at most the largest bound of its sub-chunk.  Set up by the pool
+  // wave here, by another wave only when it needs more ranks (phase 3).
   float pv[kPool];
   int pr[kPool];
-  float bound;
-  {
+  float bound = -INFINITY, lm = -INFINITY;
+  int lr = 0x7fffffff;
+  auto pool_setup = [&]() {
     const bool rl = lane < n_ck;
     const float v1[4] = {C1.x, C1.y, C1.z, C1.w}, v2[4] = {C2.x, C2.y, C2.z, C2.w};
     const float v3[4] = {C3.x, C3.y, C3.z, C3.w};
@@ -446,15 +452,15 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
     const int re = rows_in_chunks + lane;
     pv[8] = (lane < n_extra && re >= c_lo && re < c_hi) ? sanitize(XE) : -INFINITY;
     pr[8] = re;
-  }
-  bound = wave_allreduce(bound, OpMax());
-  // lane maximum (score, then lowest block among equal scores)
-  float lm = pv[0];
+    bound = wave_allreduce(bound, OpMax());
+    // lane maximum (score, then lowest block among equal scores)
+    lm = pv[0];
 #pragma unroll
-  for (int e = 1; e < kPool; ++e) lm = fmaxf(lm, pv[e]);
-  int lr = 0x7fffffff;
+    for (int e = 1; e < kPool; ++e) lm = fmaxf(lm, pv[e]);
+    lr = 0x7fffffff;
 #pragma unroll
-  for (int e = 0; e < kPool; ++e) lr = (pv[e] == lm && pr[e] < lr) ? pr[e] : lr;
+    for (int e = 0; e < kPool; ++e) lr = (pv[e] == lm && pr[e] < lr) ? pr[e] : lr;
+  };
   // Ranks of the pool's top K: the candidates are the entries >= the K-th
   // largest lane maximum (at least K of them, the top K among them),
   // compacted in lane order into this wave's LDS list, then lane c holds
@@ -486,34 +492,73 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
     __builtin_amdgcn_wave_barrier();                  // reads done before the list is rewritten
     return n_c;
   };
-  // the first NW ranks now, and this wave's content tile of the decode: rank
-  // rho (content item rho is item nf_items + rho, on wave (nf_items + rho) % NW)
+  // this wave's content tile of the decode: rank rho (content item rho is item
+  // nf_items + rho, on wave (nf_items + rho) % NW), loaded once the ranks are known
   const int rho = (wu - nf_items % NW + NW) % NW;
   int n_pre = -1;
   TileBuf<D> CA;
   int ca0 = 0, ca1 = 1, cablk = -1;
-  if (pool_ok) {
-    n_pre = pool_rank(NW);
+  auto prefetch_content = [&]() {
     if (n_sub == 1 && rho < n_pre) {
       const uint64_t hit = __ballot(prank == rho);
       cablk = min(max(key_index(readlane_u64(pk, (int)__builtin_ctzll(hit))), 0), nb - 1);
       tokens(cablk, 0, ca0, ca1);
       tile_load<D>(kbase, vbase, row_bytes, ca0, ca1, CA);
     }
+  };
+  // with entropy weights to compute the pool wave ranks alone; otherwise
+  // (fixed budget, nucleus weights from their own kernel) every wave does
+  const bool own_pool = !adaptive || wu == kPoolWave;
+  if (own_pool && pool_ok) {
+    pool_setup();
+    n_pre = pool_rank(NW);
+    prefetch_content();
+    L.pool_pk[lane] = pk;
+    L.pool_rank[lane] = prank;
+    if (lane == 0) {
+      L.pool_n = n_pre;
+      L.pool_bound = bound;
+    }
   }
   const float tf = (float)fmax(a.cfg.temperature, 1e-6);
+  // A head's softmax partial over its records and appended rows: each lane
+  // merges its up-front records against their common maximum (independent
+  // exponentials), then the rest one by one, then the lane group.
   auto merge_head = [&](int hh, const float4 (&Q)[kRecsUpFront], float X) {
     const bool on = hh < Hq;
     SoftPart pt = soft_empty();
     if (on) {
+      const float zx = hl < n_extra ? (tf == 1.f ? X : __fdiv_rn(X, tf)) : -INFINITY;
+      float M = zx;
 #pragma unroll
       for (int u = 0; u < kRecsUpFront; ++u)
-        if (hl + LPH * u < n_ck) pt = soft_merge(pt, SoftPart{Q[u].x, Q[u].y, Q[u].z});
-      for (int j = hl + LPH * kRecsUpFront; j < n_ck; j += LPH) {   // long contexts
-        const float4 q4 = rec4(hh, j, 0);
-        pt = soft_merge(pt, SoftPart{q4.x, q4.y, q4.z});
+        if (hl + LPH * u < n_ck) M = fmaxf(M, Q[u].x);
+      if (M != -INFINITY) {
+        float S = 0.f, T = 0.f;
+#pragma unroll
+        for (int u = 0; u < kRecsUpFront; ++u)
+          if (hl + LPH * u < n_ck && Q[u].x != -INFINITY) {
+            const float dm = Q[u].x - M, f = __expf(dm);
+            S = fmaf(Q[u].y, f, S);
+            T = fmaf(f, fmaf(dm, Q[u].y, Q[u].z), T);
+          }
+        if (zx != -INFINITY) {
+          const float dz = zx - M, f = __expf(dz);
+          S += f;
+          T = fmaf(f, dz, T);
+        }
+        pt = SoftPart{M, S, T};
       }
-      if (hl < n_extra) pt = soft_merge(pt, SoftPart{tf == 1.f ? X : __fdiv_rn(X, tf), 1.f, 0.f});
+      // long contexts: kRecsUpFront more records per lane at a time, their
+      // loads issued together
+      for (int j0 = hl + LPH * kRecsUpFront; j0 < n_ck; j0 += LPH * kRecsUpFront) {
+        float4 Q2[kRecsUpFront];
+#pragma unroll
+        for (int u = 0; u < kRecsUpFront; ++u) Q2[u] = rec4(hh, j0 + LPH * u, 0);
+#pragma unroll
+        for (int u = 0; u < kRecsUpFront; ++u)
+          if (j0 + LPH * u < n_ck) pt = soft_merge(pt, SoftPart{Q2[u].x, Q2[u].y, Q2[u].z});
+      }
       for (int e = hl + LPH; e < n_extra; e += LPH) {
         const float x = extra(hh, e);
         pt = soft_merge(pt, SoftPart{tf == 1.f ? x : __fdiv_rn(x, tf), 1.f, 0.f});
@@ -529,14 +574,16 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
     if (on && hl == 0) s_w[hh] = entropy_weight(pt, lognb);
   };
   if (adaptive) {
-    merge_head(hh0, R, X0);
-    for (int p = 1; p * div_u(NT, LPH) < Hq; ++p) {    // more heads than NT / LPH
-      const int hh = p * div_u(NT, LPH) + div_u(tid, LPH);
-      const int hs = min(hh, Hq - 1);
-      float4 Q[kRecsUpFront];
+    if (wu < kPoolWave) {
+      merge_head(hh0, R, X0);
+      for (int p = 1; p * div_u(kWeightLanes, LPH) < Hq; ++p) {    // more heads than the weight lanes hold
+        const int hh = p * div_u(kWeightLanes, LPH) + div_u(tid, LPH);
+        const int hs = min(hh, Hq - 1);
+        float4 Q[kRecsUpFront];
 #pragma unroll
-      for (int u = 0; u < kRecsUpFront; ++u) Q[u] = rec4(hs, hl + LPH * u, 0);
-      merge_head(hh, Q, extra(hs, hl));
+        for (int u = 0; u < kRecsUpFront; ++u) Q[u] = rec4(hs, hl + LPH * u, 0);
+        merge_head(hh, Q, extra(hs, hl));
+      }
     }
   } else if (nucleus) {
     if (tid < Hq) s_w[tid] = W0;
@@ -544,6 +591,14 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   }
   if (tid < D / 8) *reinterpret_cast<uint4*>(&L.q[8 * tid]) = qv;
   lds_barrier();
+  // the other waves take the pool wave's ranks and prefetch their content tiles
+  if (!own_pool && pool_ok) {
+    n_pre = L.pool_n;
+    bound = L.pool_bound;
+    pk = L.pool_pk[lane];
+    prank = L.pool_rank[lane];
+    prefetch_content();
+  }
 
   // ---- 2. the head's count (every wave) ----
   const bool weighted = adaptive || nucleus;
@@ -562,7 +617,11 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   // it can rank among them: every bound below the KC-th score
   bool use_pool = false;
   if (KC > 0 && pool_ok && KC <= kFastKC) {
-    const int n_c = KC <= NW ? n_pre : pool_rank(KC);
+    int n_c = n_pre;
+    if (KC > NW) {
+      if (!own_pool) pool_setup();
+      n_c = pool_rank(KC);
+    }
     if (n_c >= KC) {
       const uint64_t hit = __ballot(prank == KC - 1);
       const uint64_t kth = readlane_u64(pk, (int)__builtin_ctzll(hit));
