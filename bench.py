@@ -673,7 +673,7 @@ def main():
     copy_gbps = stream_copy_gbps(torch)
     log(f"stream copy: {copy_gbps:.0f} GB/s")
     traffic = profiled_traffic(os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                                            "score_kernel_128k_pmc.md"))
+                                            "decode_step_kernels_128k_pmc.md"))
 
     dense_us = None
     if not args.no_dense:
