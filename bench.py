@@ -69,6 +69,8 @@ def parse():
     ap.add_argument("--h2o-len", type=int, default=8192, help="prompt length of the H2O importance leg")
     ap.add_argument("--model-step", action="store_true",
                     help="BASELINE config 5 instead: a Llama-3-70B-shaped 80-layer decode step through patch_model")
+    ap.add_argument("--no-model-step", action="store_true",
+                    help="skip the config-5 model-step leg of the default run")
     ap.add_argument("--model-layers", type=int, default=80)
     ap.add_argument("--model-batch", type=int, default=4)
     ap.add_argument("--model-ctx", type=int, default=65536)
@@ -620,7 +622,9 @@ def model_step(args):
         "speedup_vs_dense_hip_step": round(t_dense_hip / t_adakv, 3),
         "speedup_vs_dense_sdpa_step": round(t_dense / t_adakv, 3),
     }
-    print(json.dumps(res), flush=True)
+    del model, cache
+    torch.cuda.empty_cache()
+    return res
 
 
 def main():
@@ -636,7 +640,7 @@ def main():
     _capi.load()
     assert torch.cuda.is_available(), "bench.py needs a ROCm device"
     if args.model_step:
-        model_step(args)
+        print(json.dumps(model_step(args)), flush=True)
         return
     log(f"device {torch.cuda.get_device_name(0)}; building {args.layers} layers at ctx {args.ctx}")
     w = Workload(torch, ops, args.ctx, args.layers, args.avg_budget, args.seed)
@@ -806,7 +810,16 @@ def main():
         "ctx_sweep": sweep,
         "ragged_batch": ragged,
         "eviction": evict,
+        "model_step": None,
     }
+    if not args.no_model_step:
+        # BASELINE config 5 (80-layer, 70B-shaped model through patch_model),
+        # after the layer workload's memory is released: its weights and cache
+        # take 211 GiB
+        del w
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        res["model_step"] = model_step(args)
     print(json.dumps(res), flush=True)
 
 
