@@ -750,7 +750,8 @@ def main():
             a_us, d_us = ms1 * 1e3 / (16 * ws.L), ms2 * 1e3 / (4 * ws.L)
             sweep.append({"context": ctx, "adakv_us_per_layer": round(a_us, 2),
                           "dense_us_per_layer": round(d_us, 2), "speedup": round(d_us / a_us, 2),
-                          "path": "fused (2 launches)" if ws.nb <= 8192 else "plan + decode (3 launches)"})
+                          # the fused select + decode kernel serves up to 16384 blocks (512 threads x 32)
+                          "path": "fused (2 launches)" if ws.nb <= 16384 else "plan + decode (3 launches)"})
             log(f"ctx {ctx}: adakv {a_us:.2f} us/layer, dense {d_us:.2f} us/layer")
             del g1, g2, ws
             torch.cuda.empty_cache()
