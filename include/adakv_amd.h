@@ -89,7 +89,7 @@ enum { ADAKV_POLICY_FIXED = 0, ADAKV_POLICY_ADAPTIVE = 1, ADAKV_POLICY_NUCLEUS =
 typedef struct {
   int32_t batch;        /* sequences in the batch (<= 4096, batch*n_kv_heads <= 12288) */
   int32_t n_q_heads;
-  int32_t n_kv_heads;   /* n_q_heads / n_kv_heads <= 8                             */
+  int32_t n_kv_heads;   /* n_q_heads / n_kv_heads <= 16                            */
   int32_t head_dim;     /* 32, 64, 128 or 256                                      */
   int32_t block_size;   /* tokens per KV block, 1..256                             */
   int32_t max_seq_len;  /* token capacity of the K/V views                         */
