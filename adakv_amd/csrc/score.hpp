@@ -421,23 +421,25 @@ __device__ __forceinline__ void score_chunk_mfma(const ScoreArgs& a, int b, int 
   }
   __syncthreads();
   if (w == 0 && lane < G) {
-    // the workgroup's record: the 4 sub-chunk partials rescaled to their common max
+    // the workgroup's record: the 4 sub-chunk partials rescaled to their common
+    // max.  Every wave's partial is read first and combined without branches
+    // (a branch per partial serialised the LDS round trips); an empty partial
+    // (m = -inf, S = T = 0) adds exactly zero.
+    float4 pm[NWV];
+#pragma unroll
+    for (int ww = 0; ww < NWV; ++ww) pm[ww] = *reinterpret_cast<const float4*>(&s_pm[ww][lane][0]);
+    const Top2 t4[4] = {s_tp[0][lane], s_tp[1][lane], s_tp[2][lane], s_tp[3][lane]};
     float M = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < NWV; ++ww) M = fmaxf(M, s_pm[ww][lane][0]);
+    for (int ww = 0; ww < NWV; ++ww) M = fmaxf(M, pm[ww].x);
     float SS = 0.f, TT = 0.f;
-    if (M != -INFINITY) {
 #pragma unroll
-      for (int ww = 0; ww < NWV; ++ww) {
-        const float mw = s_pm[ww][lane][0];
-        if (mw != -INFINITY) {
-          const float d = mw - M, f = __expf(d);
-          SS += s_pm[ww][lane][1] * f;
-          TT += f * fmaf(d, s_pm[ww][lane][1], s_pm[ww][lane][2]);
-        }
-      }
+    for (int ww = 0; ww < NWV; ++ww) {
+      const bool on = pm[ww].x != -INFINITY;
+      const float d = on ? pm[ww].x - M : 0.f, f = on ? __expf(d) : 0.f;
+      SS += pm[ww].y * f;
+      TT += f * fmaf(d, pm[ww].y, pm[ww].z);
     }
-    const Top2 t4[4] = {s_tp[0][lane], s_tp[1][lane], s_tp[2][lane], s_tp[3][lane]};
     write_part(a, b, kvh * G + lane, unit, M, SS, TT, t4);
   }
 }
@@ -454,7 +456,7 @@ __global__ __launch_bounds__(kNT) void score_kernel(ScoreArgs a) {
   __shared__ float s_q[GMAX][D];
   __shared__ float s_sc[kMfma ? 1 : GMAX * CBV];
   __shared__ float s_red[GMAX][kNT / kWave];
-  __shared__ float s_pm[kNT / kWave][GMAX][4];
+  __shared__ __align__(16) float s_pm[kNT / kWave][GMAX][4];
   __shared__ Top2 s_tp[kNT / kWave][GMAX];
 
   int id = blockIdx.x;
