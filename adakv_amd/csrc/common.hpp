@@ -224,11 +224,43 @@ __device__ __forceinline__ float wave_allreduce(float x, Op op) {
 }
 
 // ---- wave64 reductions -------------------------------------------------------
+// Sum over the wave (every lane receives it) of a 4- or 8-byte value: the
+// DPP / permlane butterfly of group_sum on each 32-bit half (a __shfl_xor
+// butterfly goes through ds_bpermute: one LDS round trip per step and half).
+// Every lane adds the same two terms at each step, so all lanes agree.
 template <typename T>
 __device__ __forceinline__ T wave_sum(T x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  return x;
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit values");
+  using U = typename std::conditional<sizeof(T) == 8, uint64_t, uint32_t>::type;
+  auto mov = [](T v, auto ctrl) -> T {
+    constexpr int C = decltype(ctrl)::value;
+    const U u = __builtin_bit_cast(U, v);
+    U r = (U)__float_as_uint(dpp_mov<C>(__uint_as_float((uint32_t)u)));
+    if constexpr (sizeof(T) == 8)
+      r |= (U)__float_as_uint(dpp_mov<C>(__uint_as_float((uint32_t)(u >> 32)))) << 32;
+    return __builtin_bit_cast(T, r);
+  };
+  auto swap_add = [](T v, bool wide) -> T {
+    const U u = __builtin_bit_cast(U, v);
+    auto sw = [&](uint32_t h) {
+      return wide ? __builtin_amdgcn_permlane32_swap(h, h, false, false)
+                  : __builtin_amdgcn_permlane16_swap(h, h, false, false);
+    };
+    const auto lo = sw((uint32_t)u);
+    U a = (U)lo[0], b = (U)lo[1];
+    if constexpr (sizeof(T) == 8) {
+      const auto hi = sw((uint32_t)(u >> 32));
+      a |= (U)hi[0] << 32;
+      b |= (U)hi[1] << 32;
+    }
+    return __builtin_bit_cast(T, a) + __builtin_bit_cast(T, b);
+  };
+  x += mov(x, std::integral_constant<int, 0xB1>{});
+  x += mov(x, std::integral_constant<int, 0x4E>{});
+  x += mov(x, std::integral_constant<int, 0x141>{});
+  x += mov(x, std::integral_constant<int, 0x140>{});
+  x = swap_add(x, false);
+  return swap_add(x, true);
 }
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll

@@ -224,14 +224,31 @@ struct NucleusLds {
   uint32_t prefix;
 };
 
+// Exclusive prefix sum over the wave of 64-bit integers: DPP row shifts on
+// both halves within each 16-lane row, then the row totals by readlane (as
+// wave_incl_scan).  Integer sums: exact in any order.  (A __shfl_up scan
+// goes through ds_bpermute, one LDS round trip per step and half.)
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_row_shr_u64(unsigned long long v) {
+  const uint32_t lo = (uint32_t)dpp_row_shr<CTRL>((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)dpp_row_shr<CTRL>((int)(uint32_t)(v >> 32));
+  return ((unsigned long long)hi << 32) | lo;
+}
 __device__ __forceinline__ unsigned long long wave_excl_scan_u64(unsigned long long x) {
   const int lane = threadIdx.x & (kWave - 1);
   unsigned long long inc = x;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const unsigned long long y = __shfl_up(inc, o);
-    if (lane >= o) inc += y;
-  }
+  inc += dpp_row_shr_u64<0x111>(inc);
+  inc += dpp_row_shr_u64<0x112>(inc);
+  inc += dpp_row_shr_u64<0x114>(inc);
+  inc += dpp_row_shr_u64<0x118>(inc);
+  auto lane_u64 = [&](int l) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)inc, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(inc >> 32), l);
+    return ((unsigned long long)hi << 32) | lo;
+  };
+  const unsigned long long r0 = lane_u64(15), r1 = lane_u64(31), r2 = lane_u64(47);
+  const int row = lane >> 4;
+  inc += (row >= 1 ? r0 : 0ull) + (row >= 2 ? r1 : 0ull) + (row >= 3 ? r2 : 0ull);
   return inc - x;
 }
 
