@@ -304,12 +304,32 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // ---- workgroup reductions (NT threads, scratch of >= NT/64 slots) ------------
+// All-lane reduction over the wave of a 4-byte value with a symmetric op
+// (DPP moves, then the permlane swaps; no LDS traffic).
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_allreduce_b32(T x, Op op) {
+  static_assert(sizeof(T) == 4, "4-byte values");
+  auto mov = [](T v, auto ctrl) -> T {
+    constexpr int C = decltype(ctrl)::value;
+    return __builtin_bit_cast(T, __float_as_uint(dpp_mov<C>(__uint_as_float(__builtin_bit_cast(uint32_t, v)))));
+  };
+  x = op(x, mov(x, std::integral_constant<int, 0xB1>{}));
+  x = op(x, mov(x, std::integral_constant<int, 0x4E>{}));
+  x = op(x, mov(x, std::integral_constant<int, 0x141>{}));
+  x = op(x, mov(x, std::integral_constant<int, 0x140>{}));
+  uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = op(__builtin_bit_cast(T, (uint32_t)r16[0]), __builtin_bit_cast(T, (uint32_t)r16[1]));
+  u = __builtin_bit_cast(uint32_t, x);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return op(__builtin_bit_cast(T, (uint32_t)r32[0]), __builtin_bit_cast(T, (uint32_t)r32[1]));
+}
+
 template <int NT, typename T, typename Op>
 __device__ __forceinline__ T block_reduce(T x, T* scratch, Op op) {
   constexpr int NW = NT / kWave;
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = op(x, __shfl_xor(x, o));
+  x = wave_allreduce_b32(x, op);
   __syncthreads();
   if (lane == 0) scratch[w] = x;
   __syncthreads();
