@@ -634,7 +634,7 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   // full path: every score of the head (thread t owns blocks [t*IPT,
   // (t+1)*IPT)); the ranked candidates (ck, cr) or the general selection's list
   constexpr int kBig = 1 << 30;
-  bool fast = false;
+  bool fast = false, split = false;
   uint64_t ck0 = 0, ck1 = 0;
   int cr0 = kBig, cr1 = kBig;
   if (KC > 0 && !use_pool) {
@@ -720,7 +720,14 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
         n_cand += max(wn[ww], 0);
       }
       fast = !over && n_cand <= kCap;
-      if (fast) {
+      // (the split ranking below in the 512-thread kernel of large budgets,
+      // where eight waves would each rank every candidate: measured at
+      // avg_budget 32, 29.3 -> 28.2 us per step; in the 256-thread kernel of
+      // small budgets its code cost the step ~0.1 us)
+      split = NT == 512 && fast;
+      if (fast && !split) {
+        // every wave ranks all candidates in registers (candidate c on lane
+        // c % 64 of ck0 / ck1; the block of rank r a ballot away)
         auto fetch = [&](int idx) -> uint64_t {   // candidate idx of the concatenated lists
           int src = 0;
 #pragma unroll
@@ -748,6 +755,43 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
           if (cr0 < KC) trow[nf + cr0] = key_index(ck0);
           if (cr1 < KC) trow[nf + cr1] = key_index(ck1);
         }
+      } else if (fast) {
+        // Many candidates: their exact ranks split over the waves (every wave
+        // ranking every candidate cost up to 128 dependent readlane steps
+        // per wave): the per-wave lists are first made one contiguous list
+        // in L.keys; lane (c, part) of wave w then takes candidate w*CPW + c
+        // and counts the keys of its part of the list above it; the parts'
+        // counts meet through the lane swaps; the block of rank r goes to
+        // L.list[r] (and to the table for r < KC).
+        constexpr int CPW = kCap / NW;              // candidates per wave
+        constexpr int PARTS = kWave / CPW;          // lane groups per candidate
+        static_assert(CPW * NW == kCap && PARTS * CPW == kWave && (PARTS == 2 || PARTS == 4), "rank split");
+        int off = 0;
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) off += ww < wu ? wn[ww] : 0;
+        if (lane < wn[wu]) L.keys[off + lane] = L.cand[wu][lane];
+        if (lane + kWave < wn[wu]) L.keys[off + lane + kWave] = L.cand[wu][lane + kWave];
+        lds_barrier();
+        const int c_local = lane % CPW, part = lane / CPW;
+        const int ci = wu * CPW + c_local;
+        const uint64_t key = L.keys[min(ci, kCap - 1)];
+        const int per = (n_cand + PARTS - 1) / PARTS;
+        const int j1 = min((part + 1) * per, n_cand);
+        int r = 0;
+        for (int j = part * per; j < j1; ++j) r += L.keys[j] > key;
+        {
+          LanePair q = swap32(__int_as_float(r));
+          r = __float_as_int(q.a) + __float_as_int(q.b);
+          if constexpr (PARTS == 4) {
+            q = swap16(__int_as_float(r));
+            r = __float_as_int(q.a) + __float_as_int(q.b);
+          }
+        }
+        if (part == 0 && ci < n_cand) {
+          L.list[r] = key_index(key);
+          if (r < KC) trow[nf + r] = key_index(key);
+        }
+        lds_barrier();
       }
     }
     if (!fast) {
@@ -805,13 +849,13 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
         const uint64_t hit = __ballot(prank == r);
         return key_index(readlane_u64(pk, hit ? (int)__builtin_ctzll(hit) : 0));
       }
-      if (fast) {
+      if (fast && !split) {
         const uint64_t h0 = __ballot(cr0 == r);
         if (h0) return key_index(readlane_u64(ck0, (int)__builtin_ctzll(h0)));
         const uint64_t h1 = __ballot(cr1 == r);
         return key_index(readlane_u64(ck1, h1 ? (int)__builtin_ctzll(h1) : 0));
       }
-      return L.list[r];
+      return L.list[r];                      // split fast path and general path
     };
     // up to three tiles in flight: item n + 3's load is issued right after
     // item n's compute; the first item may be the tile prefetched before the
