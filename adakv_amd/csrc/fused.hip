@@ -381,6 +381,19 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   const bool pool_ok = n_ck <= kWave && n_extra <= kWave;
   const float4 C1 = rec4(h, lane, 1), C2 = rec4(h, lane, 2), C3 = rec4(h, lane, 3), C4 = rec4(h, lane, 4);
   const float XE = extra(h, lane);
+  // (b') the 512-thread kernel serves large budgets, whose heads mostly take
+  //      the full selection: this head's scores are loaded now (thread t owns
+  //      blocks [t*IPT, (t+1)*IPT)) rather than after the count
+  constexpr bool kPreScores = NT == 512;
+  float vpre[kPreScores ? IPT : 1];
+  if constexpr (kPreScores) {
+    const float* srow = scores_b + h * a.sp;
+#pragma unroll
+    for (int i = 0; i < IPT; i += 4) {
+      const float4 f = *reinterpret_cast<const float4*>(srow + min(tid * IPT + i, a.sp - 4));
+      vpre[i] = f.x; vpre[i + 1] = f.y; vpre[i + 2] = f.z; vpre[i + 3] = f.w;
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
   // (c) the query (same 16-bit type as K, 16-byte aligned rows): 16 bytes per
   //     thread of the first D / 8, stored to LDS at the end of phase 1 (a store
@@ -640,7 +653,10 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
   if (KC > 0 && !use_pool) {
     const int base = tid * IPT;
     float v[IPT];
-    {
+    if constexpr (kPreScores) {
+#pragma unroll
+      for (int i = 0; i < IPT; ++i) v[i] = vpre[i];
+    } else {
       const float* srow = scores_b + h * a.sp;
 #pragma unroll
       for (int i = 0; i < IPT; i += 4) {
