@@ -165,36 +165,61 @@ __device__ __forceinline__ float kth_largest(const float* mv, int n, int KC) {
   return found == KC ? fmaxf(kth, -FLT_MAX) : -FLT_MAX;
 }
 
-// A lower bound of the KC-th largest of mv[0, n), by one wave (its own LDS
-// histograms, no workgroup barrier): two radix passes over the order-
-// preserving keys of the values (the top byte, then the next byte within the
-// bin that holds the KC-th largest) give the 16-bit key prefix of the KC-th
-// largest; the bound is the smallest float with that prefix.  -FLT_MAX when
-// fewer than KC values are finite (> -inf).
-__device__ __forceinline__ float kth_largest_radix(const float* mv, int n, int KC, int* hist, int* rd) {
+// A lower bound of the KC-th largest of mv[0, N), by one wave (its own LDS
+// histograms, no workgroup barrier): the order-preserving keys of the values
+// share a common leading prefix (the bits where the largest and smallest key
+// agree); two radix passes over the two bytes just below it (the first, then
+// the next within the bin that holds the KC-th largest) fix the prefix of the
+// KC-th largest through those 16 bits; the bound is the smallest float with
+// that prefix.  (Digits taken below the shared prefix spread the atomics over
+// the bins: the top byte, shared by nearly every value, put all of them on
+// one or two addresses.)  -FLT_MAX when fewer than KC values are finite (> -inf).
+template <int N>
+__device__ __forceinline__ float kth_largest_radix(const float* mv, int KC, int* hist, int* rd) {
+  static_assert(N % kWave == 0, "whole waves of values");
+  constexpr int PER = N / kWave;
   const int lane = threadIdx.x & (kWave - 1);
+  uint32_t key[PER];
+  bool ok[PER];
+  uint32_t kmax = 0u, kmin = 0xffffffffu;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const float x = mv[lane + kWave * i];
+    ok[i] = x != -INFINITY;
+    key[i] = (uint32_t)(sel_key(x, 0) >> 32);
+    kmax = ok[i] ? max(kmax, key[i]) : kmax;
+    kmin = ok[i] ? min(kmin, key[i]) : kmin;
+  }
+  kmax = wave_allreduce_b32(kmax, [](uint32_t x, uint32_t y) { return max(x, y); });
+  kmin = wave_allreduce_b32(kmin, [](uint32_t x, uint32_t y) { return min(x, y); });
   for (int i = lane; i < 512; i += kWave) hist[i] = 0;
   __builtin_amdgcn_wave_barrier();             // a wave's LDS operations complete in order
-  for (int i = lane; i < n; i += kWave) {
-    const float x = mv[i];
-    if (x != -INFINITY) atomicAdd(&hist[(uint32_t)(sel_key(x, 0) >> 32) >> 24], 1);
-  }
+  // shared leading bits (24 at most, so that the first digit fits below them)
+  const int cp = kmax == kmin ? 24 : min(__builtin_clz(kmax ^ kmin), 24);
+  const int sh1 = 24 - cp;                     // first digit: bits [sh1, sh1 + 8)
+#pragma unroll
+  for (int i = 0; i < PER; ++i)
+    if (ok[i]) atomicAdd(&hist[(key[i] >> sh1) & 0xffu], 1);
   __builtin_amdgcn_wave_barrier();
   radix_digit(hist, KC, rd);                   // rd[0] = digit, rd[1] = count above
   __builtin_amdgcn_wave_barrier();
-  const uint32_t b1 = (uint32_t)rd[0];
+  const uint32_t d1 = (uint32_t)rd[0];
   const int above1 = rd[1];
-  for (int i = lane; i < n; i += kWave) {
-    const float x = mv[i];
-    const uint32_t key = (uint32_t)(sel_key(x, 0) >> 32);
-    if (x != -INFINITY && (key >> 24) == b1) atomicAdd(&hist[256 + ((key >> 16) & 0xffu)], 1);
+  const uint32_t top = sh1 + 8 >= 32 ? 0u : (kmax >> (sh1 + 8)) << (sh1 + 8);   // the shared prefix
+  uint32_t tk = top | (d1 << sh1);
+  bool short2 = false;
+  if (sh1 >= 8) {                              // second digit: bits [sh1 - 8, sh1)
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (ok[i] && ((key[i] >> sh1) & 0xffu) == d1) atomicAdd(&hist[256 + ((key[i] >> (sh1 - 8)) & 0xffu)], 1);
+    __builtin_amdgcn_wave_barrier();
+    radix_digit(hist + 256, KC - above1, rd + 2);
+    __builtin_amdgcn_wave_barrier();
+    tk |= (uint32_t)rd[2] << (sh1 - 8);
+    short2 = rd[3] < 0;
   }
-  __builtin_amdgcn_wave_barrier();
-  radix_digit(hist + 256, KC - above1, rd + 2);
-  __builtin_amdgcn_wave_barrier();
-  const uint32_t tk = (b1 << 24) | ((uint32_t)rd[2] << 16);
   const uint32_t u = (tk & 0x80000000u) ? (tk & 0x7fffffffu) : ~tk;
-  return (above1 < 0 || rd[3] < 0) ? -FLT_MAX : fmaxf(__uint_as_float(u), -FLT_MAX);
+  return (above1 < 0 || short2) ? -FLT_MAX : fmaxf(__uint_as_float(u), -FLT_MAX);
 }
 
 // The general selection (rare: ties leave more candidates than the fast path
@@ -693,7 +718,7 @@ __global__ __launch_bounds__(NT) void select_decode_kernel(FusedArgs fa) {
         tau = kth_largest<NT>(L.maxv, NT, KC);
       } else {
         if (wu == 0) {
-          const float t = kth_largest_radix(L.maxv, NT, KC, L.hist, L.rd);
+          const float t = kth_largest_radix<NT>(L.maxv, KC, L.hist, L.rd);
           if (lane == 0) L.tau = t;
         }
         lds_barrier();
