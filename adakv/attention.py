@@ -2,11 +2,13 @@
 (adakv/attention.py).
 
 The planner and the decode run as HIP kernels (``libadakv_amd.so``) on the
-current stream with no host synchronisation: the block table is returned at
-its static width (``adakv_table_width``) instead of ``max(sel_lens)``, which
-the reference obtains with a device->host copy (adakv/attention.py:242).
-Entries of a row past ``sel_lens[h]`` are further-ranked candidates or -1 and
-are never read.
+current stream.  ``plan_selection`` returns the reference's table width,
+``max(sel_lens)``, which takes one device->host read of the counts as the
+reference's does (adakv/attention.py:242); the decode step
+(``adakv_decode_attention``, ``adakv_decode_step``, the HF hook) plans and
+decodes in one C call at the static width (``adakv_table_width``) with no
+host synchronisation.  Entries of a row past ``sel_lens[h]`` are
+further-ranked candidates or -1 and are never read.
 
 The instrumentation (budget trace, recall) is kept with the reference's
 names; it reads the selection back to the host only while it is switched on.
@@ -235,8 +237,10 @@ def plan_selection(q, cache: AdaKVCache, avg_budget, k_min: int = 2, k_max: int 
     """Score blocks, allocate the per-head budget, select blocks
     (adakv/attention.py:149-247).  q: [Hq, D].
 
-    Returns (block_table int32 [Hq, T], sel_lens int32 [Hq]); rows hold the
-    forced sink/local blocks, then content blocks by descending score.
+    Returns (block_table int32 [Hq, max(sel_lens)], sel_lens int32 [Hq]);
+    rows hold the forced sink/local blocks, then content blocks by descending
+    score.  The width is the largest count, as the reference returns it
+    (adakv/attention.py:242-244): one read of the counts to the host.
     """
     summ = _validate(cache, estimator, budget_policy)
     budget = _budget(avg_budget, k_min, k_max, n_sink_blocks, n_local_blocks, temperature,
@@ -244,6 +248,8 @@ def plan_selection(q, cache: AdaKVCache, avg_budget, k_min: int = 2, k_max: int 
     table, lens = ops.plan(q.unsqueeze(0), summ, cache.block_size, budget,
                            seq_len=cache.seq_len, estimator=estimator)
     block_table, sel_lens = table[0], lens[0]
+    max_sel = int(sel_lens.max().item()) if sel_lens.numel() else 0
+    block_table = block_table[:, :max_sel].contiguous()
     record_selection(block_table, sel_lens, cache.n_blocks)
     return block_table, sel_lens
 

@@ -94,3 +94,50 @@ def test_decode_step_loop_full_budget_equals_dense():
         dense = _dense_one(q[0, :, 0, :], cache.k, cache.v, group, D)
         r = rel_l2(out[0, :, 0, :].double().cpu().numpy(), dense)
         assert r < 1e-4, f"step decode != dense: rel {r:.2e}"
+
+
+@pytest.mark.parametrize("name", ["cfg1_seed0", "gqa6_kmax256"])
+def test_plan_selection_table_width_is_max_sel_lens(name):
+    """``plan_selection`` returns the reference's table width, max(sel_lens)
+    (adakv/attention.py:242-244), on the inputs of the reference's own planner
+    fixtures (tests/golden/plan_*.npz, written by the reference): its rows are
+    the static-width plan's, its selection is the reference's (near-ties
+    excluded and counted), and with none excluded its shape and selected sets
+    are the golden table's."""
+    import os
+    import cases
+    import golden_check
+    from gpu_util import compare_selection
+    from adakv.attention import AdaKVCache, _budget, _validate, plan_selection
+    from adakv_amd import ops
+    say(f"plan_selection table width: {name}")
+    p = cases.params(name)
+    q, Kkv, Vkv = cases.make_inputs(name)
+    with np.load(os.path.join(golden_check.GOLDEN, f"plan_{name}.npz")) as z:
+        gbt, gsl = z["block_table"], z["sel_lens"]
+    g = golden_check.load(name)
+    cache = AdaKVCache(block_size=p["bs"]).append_prefill(torch.from_numpy(Kkv).to(DEV),
+                                                          torch.from_numpy(Vkv).to(DEV))
+    qd = torch.from_numpy(q).to(DEV)
+    bt, sl = plan_selection(qd, cache, p["avg"], k_min=p["kmin"], k_max=p["kmax"], n_sink_blocks=p["sink"],
+                            n_local_blocks=p["local"], c_min=p["cmin"], budget_policy=p["policy"])
+    budget = _budget(p["avg"], p["kmin"], p["kmax"], p["sink"], p["local"], 1.0, p["policy"], p["cmin"])
+    full, flens = ops.plan(qd.unsqueeze(0), _validate(cache, "centroid", p["policy"]), cache.block_size, budget,
+                           seq_len=cache.seq_len)
+    torch.cuda.synchronize()
+    bt, sl, full, flens = bt.cpu().numpy(), sl.cpu().numpy(), full[0].cpu().numpy(), flens[0].cpu().numpy()
+    assert bt.dtype == np.int32 and bt.flags["C_CONTIGUOUS"]
+    assert bt.shape == (q.shape[0], int(sl.max()))
+    assert full.shape[1] >= bt.shape[1] and np.array_equal(flens, sl)
+    assert np.array_equal(full[:, : bt.shape[1]], bt)
+    nb = g["scores"].shape[1]
+    lo, hi, target, _ = O.budget_bounds(nb, p["avg"], p["kmin"], p["kmax"], p["sink"], p["local"], p["cmin"])
+    excl = compare_selection(g["scores"], bt, sl, k_oracle=g["k"], w_oracle=g.get("w", np.ones(q.shape[0])),
+                             lo=lo, target=target, sink=p["sink"], local=p["local"], cmin=p["cmin"],
+                             policy=p["policy"])
+    say(f"  width {bt.shape[1]} (golden {gbt.shape[1]}), {excl} near-tie heads excluded")
+    if excl == 0:
+        assert bt.shape == gbt.shape and np.array_equal(sl, gsl)
+        for h in range(bt.shape[0]):
+            n = int(sl[h])
+            assert set(bt[h, :n].tolist()) == set(gbt[h, :n].tolist()), f"head {h}"
