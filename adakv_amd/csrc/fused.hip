@@ -293,20 +293,41 @@ __device__ void select_general(StepLds<NT, D>& L, const float* srow, int sp, int
 
 // The KC-th largest of one value per lane (x), by repeated wave maxima that
 // remove one occurrence each; -FLT_MAX when fewer than KC values are finite
-// (> -inf).  Every lane receives it.
+// (> -inf).  Every lane receives it.  x is never NaN (pool entries are
+// sanitized scores or -inf), so the rounds compare order-preserving unsigned
+// keys: an integer maximum fuses with its DPP move and needs none of the NaN
+// canonicalisation of a float maximum, and each round's maximum is read into
+// a scalar register so the loop runs on scalar control.  (The keys order -0
+// below +0 where floats compare them equal; the returned value compares
+// equal either way.)
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  x = mx(x, __float_as_uint(dpp_mov<0xB1>(__uint_as_float(x))));
+  x = mx(x, __float_as_uint(dpp_mov<0x4E>(__uint_as_float(x))));
+  x = mx(x, __float_as_uint(dpp_mov<0x141>(__uint_as_float(x))));
+  x = mx(x, __float_as_uint(dpp_mov<0x140>(__uint_as_float(x))));
+  LanePair p = swap16(__uint_as_float(x));
+  x = mx(__float_as_uint(p.a), __float_as_uint(p.b));
+  p = swap32(__uint_as_float(x));
+  return mx(__float_as_uint(p.a), __float_as_uint(p.b));
+}
 __device__ __forceinline__ float kth_of_lanes(float x, int KC) {
   const int lane = threadIdx.x & (kWave - 1);
-  float kth = -INFINITY;
+  constexpr uint32_t kNegInf = 0x007fffffu;     // the key of -inf; 0 marks a removed lane
+  const uint32_t ux = __float_as_uint(x);
+  uint32_t key = (ux & 0x80000000u) ? ~ux : (ux | 0x80000000u);
+  uint32_t kth = kNegInf;
   int found = 0;
   for (int r = 0; r < KC; ++r) {
-    const float wm = wave_allreduce(x, OpMax());
-    if (wm == -INFINITY) break;
-    const uint64_t holders = __ballot(x == wm);
-    if (lane == (int)__builtin_ctzll(holders)) x = -INFINITY;
+    const uint32_t wm = __builtin_amdgcn_readfirstlane(wave_max_u32(key));
+    if (wm <= kNegInf) break;
+    const uint64_t holders = __ballot(key == wm);
+    if (lane == (int)__builtin_ctzll(holders)) key = 0u;
     kth = wm;
     ++found;
   }
-  return found == KC ? fmaxf(kth, -FLT_MAX) : -FLT_MAX;
+  if (found != KC) return -FLT_MAX;
+  return fmaxf(__uint_as_float((kth & 0x80000000u) ? (kth & 0x7fffffffu) : ~kth), -FLT_MAX);
 }
 
 __device__ __forceinline__ int wave_min_int(int x) {
